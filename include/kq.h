@@ -1,0 +1,109 @@
+/*
+ * kq.h -- C ABI of libkq.so, the MI355X (gfx950) quantized matrix products of the Kindi Q4 path.
+ *
+ * Every entry point takes device pointers and sizes, enqueues its kernels on `stream` (a
+ * hipStream_t passed as void*; NULL = the default stream), allocates nothing, and returns 0 or a
+ * negative KQ_ERR_* code whose text kq_last_error() returns.  Arguments are validated before any
+ * launch, the way the reference validates a pack before touching native buffers
+ * (scripts/kindi_q4/kindi/q4pack.py:86-108).
+ *
+ * Weights use the Kindi losslessly repacked layout [R/8][C/256][8][block] (q4pack.py:151-160,
+ * q4kernels.h:8-10) with GGML Q4_K (type 12, 144 B / 256 weights) or Q6_K (type 14, 210 B)
+ * blocks.  Requirements: R % 8 == 0, C % 256 == 0, 256 <= C <= 61440, w 16-byte aligned.
+ *
+ * Q8_K activations are GGML block_q8_K: float d, int8 qs[256], int16 bsums[16] (292 B per 256
+ * values); N rows of C values occupy N*(C/256) consecutive blocks.
+ *
+ * Numerical contract of the Q8_K products: per (row, super-block) the integer sums are exact and
+ * the fp32 value is v = fma(d*dx, I1, -(dmin*dx)*I2) (Q4_K) or (d*dx)*I (Q6_K); the row result
+ * is a pairwise tree of the v over super-block columns in natural order.  A row's result does not
+ * depend on N or on which kernel computed it.
+ */
+#ifndef KQ_H
+#define KQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KQ_TYPE_Q4_K 12
+#define KQ_TYPE_Q6_K 14
+
+#define KQ_OK 0
+#define KQ_ERR_ARG (-1)   /* invalid shape, type, pointer or alignment */
+#define KQ_ERR_HIP (-2)   /* the HIP runtime reported an error */
+
+#define KQ_MAX_BATCH 16   /* tokens per kq_gemv_q8k call */
+
+/* Text of the last error raised on the calling thread ("" when none). */
+const char* kq_last_error(void);
+
+/* Library version, (major << 16) | minor. */
+int kq_version(void);
+
+/*
+ * y[r] = sum_j w[r][j] * x[j] with fp32 activations: Kindi's decode GEMV.
+ * Replaces the CUDA kernel q4_gemv(w, x, y, R, C, type) (scripts/kindi_q4/kindi/q4.cu:18-27) as
+ * launched by Engine.gemv (gpu4.py:95-99), and kc_matvec (kcpu4.c:337-340).  Weights decode as
+ * in q4kernels.h:12-33; the sum is fp32 (not bit-identical to the reference's order, within
+ * 1e-5 * max|y|).  x: C floats, y: R floats, both 4-byte aligned.
+ */
+int kq_gemv(const void* w, int R, int C, int type, const float* x, float* y, void* stream);
+
+/*
+ * Up to 3 matrices sharing one input, as the CPU engine's gemv(m, n, A, y, x) does
+ * (kcpu4.c:100-118).  C is common; R[i], type[i] per matrix.
+ */
+int kq_gemv_multi(int n, const void* const* w, const int* R, int C, const int* type,
+                  const float* x, float* const* y, void* stream);
+
+/*
+ * Q8_K activation quantizer (GGML quantize_row_q8_K_ref semantics; no counterpart in the
+ * reference, whose Q4 path keeps activations in fp32, q4kernels.h:37-83).  x: N rows of C floats
+ * with row stride ldx (floats), 4-byte aligned; xq: N*(C/256) blocks of 292 B, 4-byte aligned.
+ * Inputs must be finite.
+ */
+int kq_q8k_quantize(const float* x, int64_t ldx, int C, int N, void* xq, void* stream);
+
+/*
+ * Y[n][r] (row stride ldy floats) for N = 1..16 Q8_K activation rows: batch-1 decode (N = 1)
+ * and speculative-verify GEMV.  Same role as q4_gemv with quantized activations; the batched
+ * form follows the ternary engine's k_tc_mv{2,4,8}(..., y[ntok][R]) (tc.cu:306-310).
+ */
+int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, float* y,
+                int64_t ldy, void* stream);
+
+/*
+ * Prefill GEMM: Y[m][r] for M >= 1 activation rows (row stride ldy), int8 products with int32
+ * accumulation and the fp32 epilogue above.  Slot of the ternary engine's chunk GEMM
+ * k_mm_g5q (chunk.cu:820) driven by chunk.feed (chunk.py:378); the Q4 engine itself prefills
+ * token by token (gpu4.py:109-110).
+ */
+int kq_gemm_q8k(const void* w, int R, int C, int type, const void* xq, int M, float* y,
+                int64_t ldy, void* stream);
+
+/*
+ * Exact integer sub-block sums, for parity checks:
+ *   Q4_K: sums[((n*R + r)*G + g)*8 + s]  = sum_{j<32} q4 * q8 over sub-block s (q4 in 0..15)
+ *   Q6_K: sums[((n*R + r)*G + g)*16 + t] = sum_{j<16} (q6 - 32) * q8 over sub-block t
+ * computed by the same per-lane code as kq_gemv_q8k.  No reference counterpart (the reference has
+ * no integer dot); these are GGML's aux32 terms before scaling.
+ */
+int kq_subblock_sums(const void* w, int R, int C, int type, const void* xq, int N, int32_t* sums,
+                     void* stream);
+
+/*
+ * Decode rows row0 .. row0+nrows-1 to fp32 (row stride ldy floats), bit-identical to
+ * kc_dequant (kcpu4.c:341, q4kernels.h:34-36).  With nrows = 1 this is q4_embed
+ * (q4.cu:28-32, gpu4.py:100-103).
+ */
+int kq_dequant_rows(const void* w, int R, int C, int type, int row0, int nrows, float* y,
+                    int64_t ldy, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KQ_H */

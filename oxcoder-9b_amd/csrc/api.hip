@@ -1,0 +1,148 @@
+// extern "C" entry points of libkq.so (declared in include/kq.h): argument checks, then launches.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "kq_internal.h"
+
+namespace kq {
+
+static thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_ptr(const void* p, size_t align, const char* what, const char* fn) {
+    if (!p) return fail(KQ_ERR_ARG, "%s: %s is NULL", fn, what);
+    if (reinterpret_cast<uintptr_t>(p) % align)
+        return fail(KQ_ERR_ARG, "%s: %s must be %zu-byte aligned", fn, what, align);
+    return KQ_OK;
+}
+
+// Shape rules of the packed tensor (q4pack.py:97-103: rows % 8, ne0 % 256; type in {12, 14}).
+int check_matrix(const void* w, int R, int C, int type, const char* fn) {
+    if (type != KQ_TYPE_Q4_K && type != KQ_TYPE_Q6_K)
+        return fail(KQ_ERR_ARG, "%s: type %d is not Q4_K (12) or Q6_K (14)", fn, type);
+    if (R <= 0 || R % 8) return fail(KQ_ERR_ARG, "%s: R=%d must be a positive multiple of 8", fn, R);
+    if (C <= 0 || C % 256) return fail(KQ_ERR_ARG, "%s: C=%d must be a positive multiple of 256", fn, C);
+    if (C > 61440) return fail(KQ_ERR_ARG, "%s: C=%d exceeds the supported maximum 61440", fn, C);
+    return check_ptr(w, 16, "w", fn);
+}
+
+int check_launch(const char* fn) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(KQ_ERR_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    g_err[0] = 0;
+    return KQ_OK;
+}
+
+}  // namespace kq
+
+using namespace kq;
+
+#define KQ_TRY(expr)            \
+    do {                        \
+        const int _rc = (expr); \
+        if (_rc) return _rc;    \
+    } while (0)
+
+extern "C" {
+
+const char* kq_last_error(void) { return g_err; }
+
+int kq_version(void) { return (1 << 16) | 0; }
+
+int kq_gemv(const void* w, int R, int C, int type, const float* x, float* y, void* stream) {
+    static const char* fn = "kq_gemv";
+    KQ_TRY(check_matrix(w, R, C, type, fn));
+    KQ_TRY(check_ptr(x, 4, "x", fn));
+    KQ_TRY(check_ptr(y, 4, "y", fn));
+    launch_gemv_f32(static_cast<const uint8_t*>(w), R, C, type, x, y, 0, as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_gemv_multi(int n, const void* const* w, const int* R, int C, const int* type,
+                  const float* x, float* const* y, void* stream) {
+    static const char* fn = "kq_gemv_multi";
+    if (n < 1 || n > 3) return fail(KQ_ERR_ARG, "%s: n=%d must be 1..3", fn, n);
+    if (!w || !R || !type || !y) return fail(KQ_ERR_ARG, "%s: NULL array argument", fn);
+    for (int i = 0; i < n; i++) {
+        KQ_TRY(check_matrix(w[i], R[i], C, type[i], fn));
+        KQ_TRY(check_ptr(y[i], 4, "y[i]", fn));
+    }
+    KQ_TRY(check_ptr(x, 4, "x", fn));
+    for (int i = 0; i < n; i++)
+        launch_gemv_f32(static_cast<const uint8_t*>(w[i]), R[i], C, type[i], x, y[i], 0, as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_q8k_quantize(const float* x, int64_t ldx, int C, int N, void* xq, void* stream) {
+    static const char* fn = "kq_q8k_quantize";
+    if (C <= 0 || C % 256) return fail(KQ_ERR_ARG, "%s: C=%d must be a positive multiple of 256", fn, C);
+    if (N <= 0) return fail(KQ_ERR_ARG, "%s: N=%d must be positive", fn, N);
+    if (ldx < C) return fail(KQ_ERR_ARG, "%s: ldx=%lld is smaller than C=%d", fn, (long long)ldx, C);
+    if ((int64_t)N * (C / 256) > 0x7fffffffLL)
+        return fail(KQ_ERR_ARG, "%s: N*C/256 exceeds 2^31-1 blocks", fn);
+    KQ_TRY(check_ptr(x, 4, "x", fn));
+    KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    launch_q8k_quantize(x, ldx, C, N, static_cast<uint8_t*>(xq), as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, float* y,
+                int64_t ldy, void* stream) {
+    static const char* fn = "kq_gemv_q8k";
+    KQ_TRY(check_matrix(w, R, C, type, fn));
+    if (N < 1 || N > KQ_MAX_BATCH) return fail(KQ_ERR_ARG, "%s: N=%d must be 1..%d", fn, N, KQ_MAX_BATCH);
+    if (N > 1 && ldy < R) return fail(KQ_ERR_ARG, "%s: ldy=%lld is smaller than R=%d", fn, (long long)ldy, R);
+    KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    KQ_TRY(check_ptr(y, 4, "y", fn));
+    launch_gemv_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), N, y,
+                    ldy, 0, as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_gemm_q8k(const void* w, int R, int C, int type, const void* xq, int M, float* y,
+                int64_t ldy, void* stream) {
+    static const char* fn = "kq_gemm_q8k";
+    KQ_TRY(check_matrix(w, R, C, type, fn));
+    if (M < 1) return fail(KQ_ERR_ARG, "%s: M=%d must be positive", fn, M);
+    if (M > 1 && ldy < R) return fail(KQ_ERR_ARG, "%s: ldy=%lld is smaller than R=%d", fn, (long long)ldy, R);
+    KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    KQ_TRY(check_ptr(y, 4, "y", fn));
+    launch_gemv_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), M, y,
+                    ldy, 0, as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_subblock_sums(const void* w, int R, int C, int type, const void* xq, int N, int32_t* sums,
+                     void* stream) {
+    static const char* fn = "kq_subblock_sums";
+    KQ_TRY(check_matrix(w, R, C, type, fn));
+    if (N < 1) return fail(KQ_ERR_ARG, "%s: N=%d must be positive", fn, N);
+    KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    KQ_TRY(check_ptr(sums, 4, "sums", fn));
+    launch_subblock_sums(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), N,
+                         sums, as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_dequant_rows(const void* w, int R, int C, int type, int row0, int nrows, float* y,
+                    int64_t ldy, void* stream) {
+    static const char* fn = "kq_dequant_rows";
+    KQ_TRY(check_matrix(w, R, C, type, fn));
+    if (nrows < 1 || nrows > 65535) return fail(KQ_ERR_ARG, "%s: nrows=%d must be 1..65535", fn, nrows);
+    if (row0 < 0 || row0 > R - nrows)
+        return fail(KQ_ERR_ARG, "%s: rows [%d, %d) outside [0, %d)", fn, row0, row0 + nrows, R);
+    if (nrows > 1 && ldy < C) return fail(KQ_ERR_ARG, "%s: ldy=%lld is smaller than C=%d", fn, (long long)ldy, C);
+    KQ_TRY(check_ptr(y, 4, "y", fn));
+    launch_dequant_rows(static_cast<const uint8_t*>(w), R, C, type, row0, nrows, y, ldy, as_stream(stream));
+    return check_launch(fn);
+}
+
+}  // extern "C"

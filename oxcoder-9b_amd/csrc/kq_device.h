@@ -1,0 +1,121 @@
+// Device-side helpers shared by the gfx950 kernels of libkq.
+//
+// Formats (GGML block layouts, as decoded by scripts/kindi_q4/kindi/q4kernels.h:12-33):
+//   Q4_K  144 B / 256 weights: f16 d @0, f16 dmin @2, 12 B packed 6-bit scales/mins @4, 128 B nibbles @16
+//   Q6_K  210 B / 256 weights: 128 B low nibbles @0, 64 B 2-bit highs @128, 16 int8 scales @192, f16 d @208
+//   Q8_K  292 B / 256 values : f32 d @0, 256 int8 @4, 16 int16 sums of 16 consecutive quants @260
+// Weights use the Kindi 8-row interleave [R/8][G][8][block] (q4pack.py:151-160, q4kernels.h:8-10):
+// one "tile column" is the 8 blocks of rows 8t..8t+7 at super-block column g, 1152 B (Q4_K) or
+// 1680 B (Q6_K), both multiples of 16 B.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kq {
+
+constexpr int QK = 256;
+constexpr int Q4K_BYTES = 144;
+constexpr int Q6K_BYTES = 210;
+constexpr int Q8K_BYTES = 292;
+constexpr int TYPE_Q4_K = 12;
+constexpr int TYPE_Q6_K = 14;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Same vector with 4-byte alignment: global_load_dwordx4 only needs dword alignment.
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef u32x2 u32x2_a4 __attribute__((aligned(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef f32x4 f32x4_a4 __attribute__((aligned(4)));
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {            // p 16-byte aligned
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x4 ld16_a4(const uint8_t* p) {         // p 4-byte aligned
+    return *reinterpret_cast<const u32x4_a4*>(p);
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t* p) {          // p 4-byte aligned
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// 16 bytes at a 2-byte aligned address, read as dword-aligned loads and funnel-shifted.
+// Reads the dword-aligned span [p & ~3, (p & ~3) + 20): callers guarantee it lies in the buffer.
+__device__ __forceinline__ u32x4 ld16_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint8_t* q = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+    const uint32_t sh = uint32_t(a & 3);
+    const u32x4 v = ld16_a4(q);
+    const uint32_t e = ld4(q + 16);
+    u32x4 r;
+    r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    r.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    r.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
+    return r;
+}
+
+__device__ __forceinline__ float f16_lo(uint32_t u) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffffu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t u) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {  // signed int8 x4 dot, no clamp
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Byte k (0..3) of a dword.
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int k) { return (w >> (8 * k)) & 0xffu; }
+
+// Q4_K: 6-bit scales and mins of sub-blocks 2p and 2p+1 from the 12 scale bytes held in
+// dwords s0 = bytes 0..3, s1 = 4..7, s2 = 8..11 (q4kernels.h:17-18):
+//   k < 4 : sc = s[k] & 63,                      m = s[k+4] & 63
+//   k >= 4: sc = (s[k+4] & 15) | (s[k-4]>>6)<<4, m = (s[k+4] >> 4) | (s[k]>>6)<<4
+// Rearranged per dword: scale bytes of k=0..3 are s0 & 0x3f3f3f3f, of k=4..7 are
+// (s2 & 0x0f0f0f0f) | ((s0 >> 2) & 0x30303030); mins of k=0..3 are s1 & 0x3f3f3f3f, of k=4..7
+// are ((s2 >> 4) & 0x0f0f0f0f) | ((s1 >> 2) & 0x30303030).
+struct ScMin { uint32_t sc_lo, sc_hi, m_lo, m_hi; };
+__device__ __forceinline__ ScMin q4k_scmin_pair(uint32_t s0, uint32_t s1, uint32_t s2, int p) {
+    uint32_t scw, mw;
+    if (p < 2) {
+        scw = s0 & 0x3f3f3f3fu;
+        mw = s1 & 0x3f3f3f3fu;
+    } else {
+        scw = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+        mw = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+    }
+    const int k0 = (2 * p) & 3;
+    ScMin r;
+    r.sc_lo = byte_of(scw, k0);
+    r.sc_hi = byte_of(scw, k0 + 1);
+    r.m_lo = byte_of(mw, k0);
+    r.m_hi = byte_of(mw, k0 + 1);
+    return r;
+}
+
+// Wave-level helpers.  The lane order of every fp32 reduction below is part of the numerical
+// contract of the GEMV kernels (batched results must equal single-token ones bit for bit), so
+// all kernels use these and only these.
+__device__ __forceinline__ int xor_sum_i32(int v, int mask) {
+    return v + __shfl_xor(v, mask, 64);
+}
+__device__ __forceinline__ float xor_sum_f32(float v, int mask) {
+    const float o = __shfl_xor(v, mask, 64);
+    return __fadd_rn(v, o);
+}
+// Sum over the 4 lanes of a quad (lanes 4j..4j+3), exact for int32.
+__device__ __forceinline__ int quad_sum_i32(int v) {
+    v = xor_sum_i32(v, 1);
+    return xor_sum_i32(v, 2);
+}
+// Pairwise tree over the 16 super-block slots held by lane bits 2..5 (slot = lane >> 2):
+// ((s0+s1)+(s2+s3)) + ... in natural slot order.
+__device__ __forceinline__ float slot_tree_f32(float v) {
+    v = xor_sum_f32(v, 4);
+    v = xor_sum_f32(v, 8);
+    v = xor_sum_f32(v, 16);
+    return xor_sum_f32(v, 32);
+}
+
+}  // namespace kq

@@ -1,0 +1,35 @@
+// Host-side internals of libkq: status codes, error text, argument checks, launch helpers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/kq.h"
+
+namespace kq {
+
+// Records the message for kq_last_error() (thread-local) and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Validates (w, R, C, type) as a Kindi-layout quantized tensor.
+int check_matrix(const void* w, int R, int C, int type, const char* fn);
+int check_ptr(const void* p, size_t align, const char* what, const char* fn);
+
+// Reports a failed launch (hipGetLastError) as KQ_ERR_HIP.
+int check_launch(const char* fn);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline int block_bytes(int type) { return type == KQ_TYPE_Q4_K ? 144 : 210; }
+
+// Launchers implemented by the kernel translation units.  Arguments are already validated.
+void launch_q8k_quantize(const float* x, int64_t ldx, int C, int N, uint8_t* xq, hipStream_t s);
+void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N, float* y,
+                     int64_t ldy, int rows_per_wave, hipStream_t s);
+void launch_subblock_sums(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N,
+                          int32_t* sums, hipStream_t s);
+void launch_gemv_f32(const uint8_t* w, int R, int C, int type, const float* x, float* y,
+                     int rows_per_wave, hipStream_t s);
+void launch_dequant_rows(const uint8_t* w, int R, int C, int type, int row0, int nrows, float* y,
+                         int64_t ldy, hipStream_t s);
+
+}  // namespace kq

@@ -1,0 +1,80 @@
+// Q8_K activation quantizer for gfx950: one wave per 256-value block, 4 values per lane.
+//
+// Semantics (GGML quantize_row_q8_K_ref): max = signed value of the first element with the
+// largest |x|; iscale = -127/max; q = min(127, round-half-even(iscale*x)); d = 1/iscale;
+// bsums[k] = sum of q[16k..16k+15]; an all-zero block gives d = 0, q = 0, bsums = 0.
+// Division is IEEE (hipcc default), so d and the quants match the CPU bit for bit.
+#include "kq_device.h"
+#include "kq_internal.h"
+
+namespace kq {
+
+__global__ void __launch_bounds__(256)
+k_q8k_quantize(const float* __restrict__ x, int64_t ldx, int G, int nblocks, uint8_t* __restrict__ xq) {
+    const int lane = threadIdx.x & 63;
+    const int blk = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (blk >= nblocks) return;
+    const int n = blk / G, g = blk - n * G;
+    const float* xb = x + (int64_t)n * ldx + (int64_t)g * QK + 4 * lane;
+    const f32x4 v = *reinterpret_cast<const f32x4_a4*>(xb);
+
+    // First (lowest index) element of largest |x| within the lane; NaN never compares greater.
+    float amax = 0.0f, vmax = 0.0f;
+    int idx = 1 << 20;
+    {
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float ax = __builtin_fabsf(e[k]);
+            if (ax > amax) { amax = ax; vmax = e[k]; idx = 4 * lane + k; }
+        }
+    }
+    // Across lanes: larger |x| wins, ties go to the lower index.
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const float oa = __shfl_xor(amax, m, 64);
+        const float ov = __shfl_xor(vmax, m, 64);
+        const int oi = __shfl_xor(idx, m, 64);
+        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; vmax = ov; idx = oi; }
+    }
+
+    uint8_t* ob = xq + (int64_t)blk * Q8K_BYTES;
+    uint32_t packed = 0;
+    int s4 = 0;
+    float d = 0.0f;
+    if (amax != 0.0f) {
+        const float iscale = -127.0f / vmax;
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float t = __fmul_rn(iscale, e[k]);
+            int q = (int)__builtin_rintf(t);
+            q = q < 127 ? q : 127;
+            s4 += q;
+            packed |= (uint32_t)(q & 0xff) << (8 * k);
+        }
+        d = 1.0f / iscale;
+    }
+    // 16-value sums: lanes 4j..4j+3 hold values 16j..16j+15.
+    s4 += __shfl_xor(s4, 1, 64);
+    s4 += __shfl_xor(s4, 2, 64);
+    // Pack two adjacent sums (lanes 8k and 8k+4) into one dword for the store.
+    const int s_next = __shfl_xor(s4, 4, 64);
+
+    *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = packed;
+    if (lane == 0) *reinterpret_cast<float*>(ob) = d;
+    if ((lane & 7) == 0) {
+        const uint32_t pair = ((uint32_t)s4 & 0xffffu) | ((uint32_t)s_next << 16);
+        *reinterpret_cast<uint32_t*>(ob + 260 + 4 * (lane >> 3)) = pair;
+    }
+}
+
+void launch_q8k_quantize(const float* x, int64_t ldx, int C, int N, uint8_t* xq, hipStream_t s) {
+    const int G = C / QK;
+    const int nblocks = N * G;
+    const int wpb = 4;
+    dim3 grid((nblocks + wpb - 1) / wpb), block(64 * wpb);
+    hipLaunchKernelGGL(k_q8k_quantize, grid, block, 0, s, x, ldx, G, nblocks, xq);
+}
+
+}  // namespace kq

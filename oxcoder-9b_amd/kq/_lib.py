@@ -1,0 +1,77 @@
+"""ctypes bindings of libkq.so (include/kq.h) and libkqhost.so (include/kq_host.h).
+
+The libraries are built in-tree by oxcoder-9b_amd/build.py.  A missing library raises at first
+use: there is no fallback path.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBKQ = os.path.join(HERE, "libkq.so")
+LIBKQHOST = os.path.join(HERE, "libkqhost.so")
+
+# Every symbol include/kq.h declares, with (restype, argtypes).
+_vp, _i, _i64 = C.c_void_p, C.c_int, C.c_int64
+KQ_SYMBOLS = {
+    "kq_last_error": (C.c_char_p, []),
+    "kq_version": (_i, []),
+    "kq_gemv": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "kq_gemv_multi": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, C.POINTER(_vp), _vp]),
+    "kq_q8k_quantize": (_i, [_vp, _i64, _i, _i, _vp, _vp]),
+    "kq_gemv_q8k": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),
+    "kq_gemm_q8k": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),
+    "kq_subblock_sums": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _vp]),
+    "kq_dequant_rows": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _i64, _vp]),
+}
+KQHOST_SYMBOLS = {
+    "kq_host_quantize_q4k": (_i, [_vp, _i64, _i, _vp]),
+    "kq_host_quantize_q6k": (_i, [_vp, _i64, _i, _vp]),
+    "kq_host_tile": (_i, [_vp, _i64, _i, _i, _vp]),
+    "kq_host_untile": (_i, [_vp, _i64, _i, _i, _vp]),
+}
+
+KQ_OK = 0
+KQ_ERR_ARG = -1
+KQ_ERR_HIP = -2
+KQ_MAX_BATCH = 16
+
+_libs = {}
+
+
+def _load(path, symbols):
+    if path not in _libs:
+        if not os.path.exists(path):
+            raise RuntimeError("%s is not built; run `python oxcoder-9b_amd/build.py`" % os.path.basename(path))
+        lib = C.CDLL(path)
+        for name, (res, args) in symbols.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _libs[path] = lib
+    return _libs[path]
+
+
+def kq():
+    return _load(LIBKQ, KQ_SYMBOLS)
+
+
+def kqhost():
+    return _load(LIBKQHOST, KQHOST_SYMBOLS)
+
+
+class KQError(RuntimeError):
+    """A libkq call returned a nonzero status; the message is kq_last_error()."""
+
+    def __init__(self, code, msg):
+        super().__init__("%s (status %d)" % (msg, code))
+        self.code = code
+
+
+def check(rc):
+    if rc != KQ_OK:
+        msg = kq().kq_last_error()
+        msg = msg.decode() if msg else "unknown error"
+        if rc == KQ_ERR_ARG:
+            raise ValueError(msg)
+        raise KQError(rc, msg)
+    return rc

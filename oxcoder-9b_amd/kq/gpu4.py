@@ -1,0 +1,119 @@
+"""MI355X counterpart of the Kindi Q4 GPU operator surface (scripts/kindi_q4/kindi/gpu4.py).
+
+``Weights[name] -> (buf, R, C, type)`` mirrors gpu4.Weights.__getitem__ (gpu4.py:25-48): ``buf``
+is a device uint8 tensor in the Kindi 8-row layout, R/C/type int32 as in the pack index.  Here
+the tensors are registered in memory (device resident); reading a pack is not part of this path.
+
+``Engine.gemv(names, x, outs, parts_ok=False) -> 1`` mirrors gpu4.Engine.gemv (gpu4.py:95-99):
+for each name, ``outs[i][:R] = W_name @ x`` on the current stream, asynchronously, returning 1
+(the number of column parts, as the reference does).  Two numerics modes:
+
+* ``"f32"`` -- fp32 activations, the reference's numerics (kq_gemv).
+* ``"q8k"`` -- the input is quantized once to Q8_K (kq_q8k_quantize) into a preallocated
+  workspace, then every named matrix runs the int8 GEMV (kq_gemv_q8k).
+
+``gemv_batch`` (speculative verify, N <= 16 rows) and ``gemm`` (prefill chunk, any M) extend the
+same contract to several activation rows: X is [N][C] fp32, each out is [N][R] (row stride
+``out.stride(0)``), the batched layout of the ternary engine's k_tc_mv (tc.cu:306-310).
+"""
+import torch
+
+from . import ops
+from .formats import Q8K_BYTES, QK, check_shape
+
+
+class Weights:
+    def __init__(self, device="cuda"):
+        self.device = torch.device(device)
+        self.cache = {}
+
+    def add(self, name, packed, R, C, ty):
+        """Register a Kindi-layout tensor (numpy uint8 or torch uint8), copied to the device once."""
+        check_shape(R, C, ty)
+        buf = torch.as_tensor(packed, dtype=torch.uint8).reshape(-1).to(self.device)
+        if buf.numel() != R * (C // QK) * {12: 144, 14: 210}[ty]:
+            raise ValueError("Invalid packed tensor dimensions for " + name)
+        self.cache[name] = (buf, int(R), int(C), int(ty))
+        return self.cache[name]
+
+    def __getitem__(self, name):
+        return self.cache[name]
+
+    def __contains__(self, name):
+        return name in self.cache
+
+
+class Engine:
+    def __init__(self, weights, mode="q8k", max_cols=None, max_rows=16):
+        if mode not in ("q8k", "f32"):
+            raise ValueError("mode must be 'q8k' or 'f32'")
+        self.w = weights
+        self.mode = mode
+        self.device = weights.device
+        cols = max_cols or max([C for (_, _, C, _) in weights.cache.values()] or [QK])
+        self.max_cols = cols
+        self.max_rows = max_rows
+        # Q8_K workspace, preallocated like the reference's device scratch (gpu4.py:70-79).
+        self.xq = torch.empty(max_rows * (cols // QK) * Q8K_BYTES, dtype=torch.uint8, device=self.device)
+
+    def _check_out(self, y, R, N=1):
+        need = (N - 1) * (y.stride(0) if y.dim() == 2 else R) + R
+        if y.dtype != torch.float32 or y.numel() < need:
+            raise ValueError("output buffer too small or not float32")
+
+    def _quantize(self, X, C):
+        N = X.shape[0]
+        if C > self.max_cols or N > self.max_rows:
+            raise ValueError("input %dx%d exceeds the engine workspace %dx%d" % (N, C, self.max_rows, self.max_cols))
+        return ops.q8k_quantize(X, self.xq[: N * (C // QK) * Q8K_BYTES].view(N, -1))
+
+    def gemv(self, names, x, outs, parts_ok=False):
+        mats = [self.w[n] for n in names]
+        if len(outs) < len(mats):
+            raise ValueError("one output per matrix")
+        C = mats[0][2]
+        if any(m[2] != C for m in mats) or x.numel() < C:
+            raise ValueError("matrices sharing x must have the same column count")
+        for (w, R, _, _), y in zip(mats, outs):
+            self._check_out(y, R)
+        if self.mode == "f32":
+            for (w, R, C_, ty), y in zip(mats, outs):
+                ops.gemv(w, R, C_, ty, x, y)
+            return 1
+        xq = self._quantize(x.reshape(1, -1)[:, :C], C)
+        for (w, R, C_, ty), y in zip(mats, outs):
+            ops.gemv_q8k(w, R, C_, ty, xq, 1, y)
+        return 1
+
+    def gemv_batch(self, names, X, outs):
+        """Speculative-verify GEMV: X [N][C], N <= 16; out[n][r] bit-identical to gemv on row n."""
+        N, C = X.shape
+        if not 1 <= N <= 16:
+            raise ValueError("batch of %d rows: 1..16 supported" % N)
+        xq = self._quantize(X, C)
+        for name, y in zip(names, outs):
+            w, R, C_, ty = self.w[name]
+            if C_ != C:
+                raise ValueError("column count mismatch for " + name)
+            self._check_out(y, R, N)
+            ops.gemv_q8k(w, R, C_, ty, xq, N, y, y.stride(0))
+        return 1
+
+    def gemm(self, names, X, outs):
+        """Prefill GEMM over M rows of X [M][C]."""
+        M, C = X.shape
+        xq = self._quantize(X, C)
+        for name, y in zip(names, outs):
+            w, R, C_, ty = self.w[name]
+            if C_ != C:
+                raise ValueError("column count mismatch for " + name)
+            self._check_out(y, R, M)
+            ops.gemm_q8k(w, R, C_, ty, xq, M, y, y.stride(0))
+        return 1
+
+    def dequant(self, name, row, out=None):
+        """One decoded row (kc_dequant, kcpu4.c:341; q4_embed, q4.cu:28-32)."""
+        w, R, C, ty = self.w[name]
+        if not 0 <= row < R:
+            raise ValueError("Invalid row")
+        return ops.dequant_rows(w, R, C, ty, row, 1, out)[0] if out is None else ops.dequant_rows(w, R, C, ty, row, 1, out)

@@ -1,0 +1,103 @@
+"""Tensor-level calls into libkq on torch-ROCm device tensors.
+
+torch supplies device memory and the current stream; every computation runs in libkq's HIP
+kernels through the C ABI of include/kq.h.  Shapes are checked here (ValueError) before any
+launch, and a nonzero status from the library raises (ValueError for bad arguments, KQError for
+HIP failures).
+"""
+import ctypes as C
+
+import torch
+
+from . import _lib
+from .formats import BLOCK, Q8K_BYTES, QK, check_shape
+
+
+def _stream(device):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dev(t, name, dtype=None):
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError("%s must be a device tensor" % name)
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError("%s must be %s, got %s" % (name, dtype, t.dtype))
+    return C.c_void_p(t.data_ptr())
+
+
+def _weights(w, R, C_, ty):
+    check_shape(R, C_, ty)
+    if w.dtype != torch.uint8 or not w.is_contiguous():
+        raise ValueError("weights must be a contiguous uint8 tensor")
+    if w.numel() < R * (C_ // QK) * BLOCK[ty]:
+        raise ValueError("weight buffer holds %d bytes, %dx%d type %d needs %d"
+                         % (w.numel(), R, C_, ty, R * (C_ // QK) * BLOCK[ty]))
+    return _dev(w, "w")
+
+
+def gemv(w, R, C_, ty, x, y):
+    """y[R] = W x with fp32 x[C] (Kindi numerics, kq_gemv)."""
+    pw = _weights(w, R, C_, ty)
+    if x.numel() < C_ or y.numel() < R:
+        raise ValueError("x or y too small")
+    _lib.check(_lib.kq().kq_gemv(pw, R, C_, ty, _dev(x, "x", torch.float32), _dev(y, "y", torch.float32),
+                                 _stream(w.device)))
+    return y
+
+
+def q8k_quantize(x, out=None):
+    """x [N][C] fp32 (row stride x.stride(0)) -> Q8_K bytes uint8 [N][C/256*292]."""
+    if x.dim() == 1:
+        x = x.unsqueeze(0)
+    N, C_ = x.shape
+    if x.stride(1) != 1:
+        raise ValueError("x rows must be contiguous")
+    if out is None:
+        out = torch.empty((N, C_ // QK * Q8K_BYTES), dtype=torch.uint8, device=x.device)
+    elif out.numel() < N * (C_ // QK) * Q8K_BYTES:
+        raise ValueError("out too small for %d Q8_K rows of %d" % (N, C_))
+    _lib.check(_lib.kq().kq_q8k_quantize(_dev(x, "x", torch.float32), x.stride(0), C_, N,
+                                         _dev(out, "out", torch.uint8), _stream(x.device)))
+    return out
+
+
+def gemv_q8k(w, R, C_, ty, xq, N, y, ldy=None):
+    """Y[n][r] for N Q8_K activation rows (kq_gemv_q8k, N <= 16)."""
+    pw = _weights(w, R, C_, ty)
+    ldy = R if ldy is None else ldy
+    if xq.numel() < N * (C_ // QK) * Q8K_BYTES or y.numel() < (N - 1) * ldy + R:
+        raise ValueError("xq or y too small")
+    _lib.check(_lib.kq().kq_gemv_q8k(pw, R, C_, ty, _dev(xq, "xq", torch.uint8), N,
+                                     _dev(y, "y", torch.float32), ldy, _stream(w.device)))
+    return y
+
+
+def gemm_q8k(w, R, C_, ty, xq, M, y, ldy=None):
+    """Y[m][r] for M Q8_K activation rows (kq_gemm_q8k, prefill)."""
+    pw = _weights(w, R, C_, ty)
+    ldy = R if ldy is None else ldy
+    if xq.numel() < M * (C_ // QK) * Q8K_BYTES or y.numel() < (M - 1) * ldy + R:
+        raise ValueError("xq or y too small")
+    _lib.check(_lib.kq().kq_gemm_q8k(pw, R, C_, ty, _dev(xq, "xq", torch.uint8), M,
+                                     _dev(y, "y", torch.float32), ldy, _stream(w.device)))
+    return y
+
+
+def subblock_sums(w, R, C_, ty, xq, N):
+    """Exact int32 sub-block sums [N][R][G][8 or 16] (kq_subblock_sums)."""
+    pw = _weights(w, R, C_, ty)
+    nsub = 8 if ty == 12 else 16
+    S = torch.empty((N, R, C_ // QK, nsub), dtype=torch.int32, device=w.device)
+    _lib.check(_lib.kq().kq_subblock_sums(pw, R, C_, ty, _dev(xq, "xq", torch.uint8), N,
+                                          _dev(S, "S", torch.int32), _stream(w.device)))
+    return S
+
+
+def dequant_rows(w, R, C_, ty, row0, nrows, y=None):
+    """Rows row0..row0+nrows-1 decoded to fp32 [nrows][C] (kq_dequant_rows)."""
+    pw = _weights(w, R, C_, ty)
+    if y is None:
+        y = torch.empty((nrows, C_), dtype=torch.float32, device=w.device)
+    _lib.check(_lib.kq().kq_dequant_rows(pw, R, C_, ty, row0, nrows, _dev(y, "y", torch.float32),
+                                         y.stride(0) if y.dim() == 2 else C_, _stream(w.device)))
+    return y

@@ -1,0 +1,95 @@
+"""The Engine/Weights operator surface (mirror of scripts/kindi_q4/kindi/gpu4.py:17-110) on the
+GPU: results, return value, argument errors, and the full decode-layer shapes."""
+import numpy as np
+import pytest
+import torch
+
+from kq import quantize as kqq
+from kq.gpu4 import Engine, Weights
+
+pytestmark = pytest.mark.gpu
+
+LAYER = [  # name, R, C, type: one 9B-class decode layer (q, k, v, o, gate, up: Q4_K; down: Q6_K)
+    ("attn_q", 4096, 4096, 12), ("attn_k", 1024, 4096, 12), ("attn_v", 1024, 4096, 12),
+    ("attn_output", 4096, 4096, 12), ("ffn_gate", 12288, 4096, 12), ("ffn_up", 12288, 4096, 12),
+    ("ffn_down", 4096, 12288, 14),
+]
+
+
+@pytest.fixture(scope="module")
+def layer(dev):
+    w = Weights(dev)
+    host = {}
+    for i, (name, R, C, ty) in enumerate(LAYER):
+        W = kqq.synthetic_matrix(R, C, ty, seed=i)
+        host[name] = (W, R, C, ty)
+        w.add(name, W, R, C, ty)
+    return w, host
+
+
+def test_weights_tuple_contract(layer):
+    w, host = layer
+    buf, R, C, ty = w["ffn_down"]
+    assert (R, C, ty) == (4096, 12288, 14) and buf.dtype == torch.uint8 and buf.is_cuda
+    assert buf.numel() == 4096 * 48 * 210
+
+
+@pytest.mark.parametrize("mode", ["q8k", "f32"])
+def test_engine_gemv_layer(layer, orc, dev, mode):
+    """gemv(names, x, outs) -> 1 for the attention and FFN groups; outputs vs the oracle."""
+    w, host = layer
+    eng = Engine(w, mode=mode)
+    groups = [(["attn_q", "attn_k", "attn_v"], 4096), (["attn_output"], 4096),
+              (["ffn_gate", "ffn_up"], 4096), (["ffn_down"], 12288)]
+    for g, (names, C) in enumerate(groups):
+        x = kqq.synthetic_activations(1, C, seed=100 + g)[0]
+        outs = [torch.empty(host[n][1], device=dev) for n in names]
+        assert eng.gemv(names, torch.from_numpy(x).to(dev), outs) == 1
+        torch.cuda.synchronize()
+        for n, y in zip(names, outs):
+            W, R, C_, ty = host[n]
+            if mode == "q8k":
+                want = orc.gemv_q8k(W, R, C_, ty, orc.quantize_q8k(x[None]), 1)[0]
+            else:
+                want = orc.matvec_f32(W, R, C_, ty, x).astype(np.float64)
+            got = y.cpu().numpy()
+            assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max(), n
+
+
+def test_engine_batch_and_gemm_agree(layer, dev):
+    w, _ = layer
+    eng = Engine(w, mode="q8k")
+    X = torch.from_numpy(kqq.synthetic_activations(8, 4096, seed=9)).to(dev)
+    yb = torch.empty((8, 12288), device=dev)
+    ym = torch.empty((8, 12288), device=dev)
+    assert eng.gemv_batch(["ffn_gate"], X, [yb]) == 1
+    assert eng.gemm(["ffn_gate"], X, [ym]) == 1
+    y1 = torch.empty(12288, device=dev)
+    eng.gemv(["ffn_gate"], X[5], [y1])
+    torch.cuda.synchronize()
+    assert torch.equal(yb[5], y1)
+    np.testing.assert_allclose(ym.cpu().numpy(), yb.cpu().numpy(), rtol=0, atol=1e-5 * yb.abs().max().item())
+
+
+def test_engine_rejects_bad_calls(layer, dev):
+    w, _ = layer
+    eng = Engine(w, mode="q8k")
+    x = torch.zeros(4096, device=dev)
+    with pytest.raises(ValueError):
+        eng.gemv(["attn_q", "ffn_down"], x, [torch.empty(4096, device=dev), torch.empty(4096, device=dev)])
+    with pytest.raises(ValueError):
+        eng.gemv(["attn_q"], x, [torch.empty(100, device=dev)])
+    with pytest.raises(ValueError):
+        eng.gemv_batch(["attn_q"], torch.zeros((17, 4096), device=dev), [torch.empty((17, 4096), device=dev)])
+    with pytest.raises(KeyError):
+        eng.gemv(["missing"], x, [torch.empty(4096, device=dev)])
+
+
+def test_dequant_row_matches_oracle(layer, orc, dev):
+    w, host = layer
+    eng = Engine(w)
+    for name in ("attn_k", "ffn_down"):
+        W, R, C, ty = host[name]
+        row = eng.dequant(name, R - 3)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(row.cpu().numpy(), orc.dequant_row(W, R, C, ty, R - 3))

@@ -1,0 +1,208 @@
+"""Parity of the HIP kernels (through libkq's C ABI) with the CPU oracle.
+
+Bars: decode, Q8_K bytes and integer sub-block sums bit-exact; fp32 outputs within
+1e-5 * max|y_ref| (y_ref = oracle evaluated in double from the exact integer sums); batched rows
+bit-identical to the single-token result.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import reference_unit_inputs
+from kq import ops, quantize as kqq
+from kq.formats import Q4_K, Q6_K
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def dev_t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def assert_close_inf(got, want, tol=TOL):
+    scale = np.abs(want).max()
+    err = np.abs(got.astype(np.float64) - want).max()
+    assert err <= tol * scale, "max err %.3g vs %.3g * %.3g" % (err, tol, scale)
+
+
+def synth(R, C, ty, seed):
+    return kqq.synthetic_matrix(R, C, ty, seed)
+
+
+# --------------------------------------------------------------------------------------- decode
+@pytest.mark.parametrize("tag,ty", [("tq", 12), ("tq", 14), ("syn", 12), ("syn", 14)])
+def test_dequant_golden_bit_exact(dev, golden, orc, tag, ty):
+    k = "%s_%d_" % (tag, ty)
+    R, C, _ = (int(v) for v in golden[k + "shape"])
+    W = golden[k + "w"]
+    y = host(ops.dequant_rows(dev_t(W, dev), R, C, ty, 0, R))
+    for i, r in enumerate(golden[k + "rows"]):
+        np.testing.assert_array_equal(y[r], golden[k + "deq"][i])
+    np.testing.assert_array_equal(y, orc.dequant(W, R, C, ty))
+
+
+def test_dequant_single_row_offset(dev, orc):
+    R, C = 64, 2048
+    W = synth(R, C, Q6_K, 9)
+    out = torch.full((3, C + 16), -1.0, device=dev)
+    ops.dequant_rows(dev_t(W, dev), R, C, Q6_K, 37, 3, out)
+    y = host(out)
+    for i in range(3):
+        np.testing.assert_array_equal(y[i, :C], orc.dequant_row(W, R, C, Q6_K, 37 + i))
+    assert np.all(y[:, C:] == -1.0)
+
+
+# ----------------------------------------------------------------------------------------- Q8_K
+def q8k_cases():
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((6, 4096)).astype(np.float32)
+    x[1] *= 1e-3
+    x[2] *= 250.0
+    x[3, 512:768] = 0.0                               # zero block
+    x[4, :256] = 0.0
+    x[4, 0] = -127.0                                  # iscale = 1: round-half-even cases
+    x[4, 1:9] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.4999999, 126.5]
+    x[5, 256:512] = 0.0
+    x[5, 256 + 3], x[5, 256 + 10] = -5.0, 5.0         # |x| tie: first wins
+    x[5, 1024:1280] = 7.0                             # constant block
+    return x
+
+
+def test_q8k_quantize_bit_exact(dev, orc):
+    x = q8k_cases()
+    got = host(ops.q8k_quantize(dev_t(x, dev)))
+    np.testing.assert_array_equal(got, orc.quantize_q8k(x))
+
+
+def test_q8k_quantize_strided_rows(dev, orc):
+    rng = np.random.default_rng(4)
+    big = rng.standard_normal((5, 1536 + 40)).astype(np.float32)
+    xd = dev_t(big, dev)[:, :1536]
+    assert xd.stride(0) == 1576
+    got = host(ops.q8k_quantize(xd))
+    np.testing.assert_array_equal(got, orc.quantize_q8k(big[:, :1536]))
+
+
+def test_q8k_quantize_large(dev, orc):
+    """Full prefill activation size (M = 2048, K = 12288)."""
+    x = kqq.synthetic_activations(2048, 12288, seed=3)
+    got = host(ops.q8k_quantize(dev_t(x, dev)))
+    np.testing.assert_array_equal(got, orc.quantize_q8k(x))
+
+
+# --------------------------------------------------------------------------- integer sub-blocks
+@pytest.mark.parametrize("ty", [12, 14])
+def test_subblock_sums_reference_inputs(dev, orc, ty):
+    W, x, R, C = reference_unit_inputs()[ty]
+    xs = np.stack([x, -x, 3 * x]).astype(np.float32)
+    xq = orc.quantize_q8k(xs)
+    got = host(ops.subblock_sums(dev_t(W, dev), R, C, ty, dev_t(xq, dev), 3))
+    np.testing.assert_array_equal(got, orc.subblock_sums(W, R, C, ty, xq, 3))
+
+
+@pytest.mark.parametrize("ty,R,C", [(12, 64, 4096), (14, 64, 4096), (12, 16, 4352), (14, 24, 12288)])
+def test_subblock_sums_synthetic(dev, orc, ty, R, C):
+    W = synth(R, C, ty, 5)
+    xq = orc.quantize_q8k(kqq.synthetic_activations(2, C, seed=5))
+    got = host(ops.subblock_sums(dev_t(W, dev), R, C, ty, dev_t(xq, dev), 2))
+    np.testing.assert_array_equal(got, orc.subblock_sums(W, R, C, ty, xq, 2))
+
+
+def test_subblock_sums_random_bytes_extremes(dev, orc):
+    """All-0xFF and random bytes: the largest integer magnitudes a block can produce."""
+    rng = np.random.default_rng(8)
+    for ty, bs in ((12, 144), (14, 210)):
+        R, C = 16, 1024
+        W = rng.integers(0, 256, R * 4 * bs, dtype=np.uint8)
+        W[: 8 * bs] = 0xFF
+        x = np.full((1, C), -1.0, np.float32)   # every q8 = +127 after the sign convention
+        xq = orc.quantize_q8k(x)
+        got = host(ops.subblock_sums(dev_t(W, dev), R, C, ty, dev_t(xq, dev), 1))
+        np.testing.assert_array_equal(got, orc.subblock_sums(W, R, C, ty, xq, 1))
+
+
+# ------------------------------------------------------------------------------------ Q8_K GEMV
+GEMV_SHAPES = [
+    (12, 8, 256), (14, 8, 256),            # one super-block column
+    (12, 40, 4352), (14, 40, 4352),        # G = 17: two column passes, ragged
+    (12, 4096, 4096),                      # single Q4_K GEMV, W 4096 x 4096
+    (12, 1024, 4096), (12, 12288, 4096),   # k/v and gate/up shapes
+    (14, 4096, 12288),                     # Q6_K down
+    (14, 1024, 4096),                      # Q6_K attn_v
+]
+
+
+@pytest.mark.parametrize("ty,R,C", GEMV_SHAPES)
+def test_gemv_q8k_vs_oracle(dev, orc, ty, R, C):
+    W = synth(R, C, ty, R + C + ty)
+    x = kqq.synthetic_activations(1, C, seed=R)
+    xq = orc.quantize_q8k(x)
+    y = torch.empty(R, device=dev)
+    ops.gemv_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), 1, y)
+    assert_close_inf(host(y), orc.gemv_q8k(W, R, C, ty, xq, 1)[0])
+
+
+@pytest.mark.parametrize("ty", [12, 14])
+def test_gemv_q8k_reference_inputs(dev, orc, ty):
+    W, x, R, C = reference_unit_inputs()[ty]
+    xq = orc.quantize_q8k(x[None])
+    y = torch.empty(R, device=dev)
+    ops.gemv_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), 1, y)
+    assert_close_inf(host(y), orc.gemv_q8k(W, R, C, ty, xq, 1)[0])
+
+
+@pytest.mark.parametrize("ty,R,C", [(12, 12288, 4096), (14, 4096, 12288), (12, 64, 4352)])
+def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
+    """Speculative-verify invariant: every row of a batch equals its N = 1 result bit for bit."""
+    W = dev_t(synth(R, C, ty, 77), dev)
+    X = kqq.synthetic_activations(16, C, seed=C)
+    xq = orc.quantize_q8k(X)
+    xqd = dev_t(xq, dev)
+    single = torch.empty((16, R), device=dev)
+    for n in range(16):
+        ops.gemv_q8k(W, R, C, ty, xqd[n:n + 1], 1, single[n])
+    s = host(single)
+    for N in (2, 3, 4, 5, 8, 13, 16):
+        yb = torch.empty((N, R + 8), device=dev)
+        ops.gemv_q8k(W, R, C, ty, xqd[:N], N, yb, R + 8)
+        np.testing.assert_array_equal(host(yb)[:, :R], s[:N])
+    assert_close_inf(s, orc.gemv_q8k(host(W), R, C, ty, xq, 16))
+
+
+@pytest.mark.parametrize("ty,R,C,M", [(12, 512, 4096, 64), (14, 256, 12288, 40)])
+def test_gemm_q8k_vs_oracle(dev, orc, ty, R, C, M):
+    W = synth(R, C, ty, 31)
+    X = kqq.synthetic_activations(M, C, seed=M)
+    xq = orc.quantize_q8k(X)
+    y = torch.empty((M, R), device=dev)
+    ops.gemm_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), M, y)
+    assert_close_inf(host(y), orc.gemv_q8k(W, R, C, ty, xq, M))
+
+
+# ------------------------------------------------------------------------------- fp32-x GEMV
+@pytest.mark.parametrize("ty", [12, 14])
+def test_gemv_f32_reference_unit_test(dev, orc, ty):
+    """The reference unit test (test_quant.py:30-32) on the GPU drop-in, plus the tier bar
+    against the restated q4_dot."""
+    W, x, R, C = reference_unit_inputs()[ty]
+    y = torch.empty(R, device=dev)
+    ops.gemv(dev_t(W, dev), R, C, ty, dev_t(x, dev), y)
+    got = host(y)
+    dense = orc.dequant(W, R, C, ty).astype(np.float64)
+    np.testing.assert_allclose(got, dense @ x.astype(np.float64), atol=0.00015, rtol=0.00001)
+    assert_close_inf(got, orc.matvec_f32(W, R, C, ty, x).astype(np.float64))
+
+
+@pytest.mark.parametrize("ty,R,C", [(12, 4096, 4096), (14, 4096, 12288), (12, 40, 4352), (14, 8, 256)])
+def test_gemv_f32_vs_oracle(dev, orc, ty, R, C):
+    W = synth(R, C, ty, 3 * R + ty)
+    x = kqq.synthetic_activations(1, C, seed=C + 1)[0]
+    y = torch.empty(R, device=dev)
+    ops.gemv(dev_t(W, dev), R, C, ty, dev_t(x, dev), y)
+    assert_close_inf(host(y), orc.matvec_f32(W, R, C, ty, x).astype(np.float64))

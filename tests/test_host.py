@@ -1,0 +1,121 @@
+"""Host-side pieces: the C ABI library loads and exports what include/*.h declares (no GPU
+compute), the synthetic quantizer, the Kindi repack, and argument validation paths."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+
+def _declared(header):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kq_\w+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header,lib", [("kq.h", "libkq.so"), ("kq_host.h", "libkqhost.so")])
+def test_library_exports_every_declared_symbol(header, lib):
+    from kq import _lib
+    path = os.path.join(ROOT, "oxcoder-9b_amd", "kq", lib)
+    assert os.path.exists(path), "build the package first"
+    so = ctypes.CDLL(path)
+    names = _declared(header)
+    assert names, header
+    for n in names:
+        assert hasattr(so, n), n
+    table = _lib.KQ_SYMBOLS if lib == "libkq.so" else _lib.KQHOST_SYMBOLS
+    assert sorted(table) == names
+
+
+def test_error_text_and_version_without_gpu():
+    """Entry points that touch no device work on a host without a GPU."""
+    from kq import _lib
+    lib = _lib.kq()
+    assert lib.kq_version() >> 16 == 1
+    assert lib.kq_last_error() == b""
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((None, 16, 512, 12), "w is NULL"),
+    ((16, 12, 512, 12), "R=12"),
+    ((16, 16, 500, 12), "C=500"),
+    ((16, 16, 512, 13), "type 13"),
+    ((8, 16, 512, 12), "16-byte aligned"),
+])
+def test_argument_errors_raise_before_launch(args, msg):
+    """Bad shapes return KQ_ERR_ARG with a message and launch nothing (host-only path)."""
+    from kq import _lib
+    lib = _lib.kq()
+    w, R, C, ty = args
+    rc = lib.kq_gemv_q8k(ctypes.c_void_p(w), R, C, ty, ctypes.c_void_p(64), 1, ctypes.c_void_p(64), R, None)
+    assert rc == _lib.KQ_ERR_ARG
+    assert msg in lib.kq_last_error().decode()
+    with pytest.raises(ValueError, match=re.escape(msg)):
+        _lib.check(rc)
+
+
+def test_batch_limit():
+    from kq import _lib
+    lib = _lib.kq()
+    rc = lib.kq_gemv_q8k(ctypes.c_void_p(256), 16, 512, 12, ctypes.c_void_p(64), 17, ctypes.c_void_p(64), 16, None)
+    assert rc == _lib.KQ_ERR_ARG and "N=17" in lib.kq_last_error().decode()
+
+
+@pytest.mark.parametrize("ty", [12, 14])
+def test_tile_round_trip_and_addressing(ty):
+    from kq import formats, quantize as kqq
+    R, C = 24, 768
+    rng = np.random.default_rng(ty)
+    raw = rng.integers(0, 256, R * (C // 256) * formats.BLOCK[ty], dtype=np.uint8)
+    t_np = formats.tile(raw, R, C, ty)
+    t_nat = kqq.tile(raw, R, C, ty)
+    np.testing.assert_array_equal(t_np, t_nat)
+    np.testing.assert_array_equal(formats.untile(t_np, R, C, ty), raw)
+    np.testing.assert_array_equal(kqq.untile(t_nat, R, C, ty), raw)
+    bs = formats.BLOCK[ty]
+    G = C // 256
+    for r, g in [(0, 0), (7, 2), (8, 1), (23, 2)]:
+        off = formats.block_offset(R, C, ty, r, g)
+        np.testing.assert_array_equal(t_np[off:off + bs], raw[(r * G + g) * bs:(r * G + g + 1) * bs])
+
+
+def test_shape_validation():
+    from kq import formats
+    for R, C, ty in [(12, 512, 12), (16, 500, 12), (16, 512, 0), (0, 512, 14)]:
+        with pytest.raises(ValueError):
+            formats.check_shape(R, C, ty)
+
+
+@pytest.mark.parametrize("ty", [12, 14])
+def test_quantizer_round_trip(orc, ty):
+    """Quantize N(0, 0.02) weights and decode with the oracle: per-weight error within the
+    quantization step of its sub-block, and small RMS error."""
+    from kq import quantize as kqq
+    R, C = 64, 2048
+    w = kqq.synthetic_fp32(R, C, seed=3)
+    W = kqq.tile(kqq.quantize(w, ty), R, C, ty)
+    deq = orc.dequant(W, R, C, ty)
+    err = np.abs(deq - w)
+    rms = np.sqrt(np.mean(err ** 2)) / 0.02
+    assert rms < (0.12 if ty == 12 else 0.03), rms
+    # step bound: Q4_K step = range/15 of a 32-block (<= 2*max|x|/15); Q6_K step = max|x|/31
+    blocks = w.reshape(R, -1, 32 if ty == 12 else 16)
+    amax = np.abs(blocks).max(-1, keepdims=True)
+    step = 2 * amax / 15 if ty == 12 else amax / 31
+    bound = np.broadcast_to(step, blocks.shape).reshape(R, C)
+    assert np.all(err <= 1.1 * bound + 1e-6)
+
+
+def test_quantizer_zero_and_constant_blocks(orc):
+    from kq import quantize as kqq
+    w = np.zeros((8, 512), np.float32)
+    w[1] = 0.5
+    w[2, :256] = -0.25
+    for ty in (12, 14):
+        W = kqq.tile(kqq.quantize(w, ty), 8, 512, ty)
+        deq = orc.dequant(W, 8, 512, ty)
+        np.testing.assert_allclose(deq, w, atol=0.5 / 31)
+        assert not deq[0].any() and not deq[3:].any()

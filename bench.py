@@ -1,0 +1,347 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized matrix products on one MI355X.
+
+Step = one 9B-class decode layer's projections at batch 1 (Q8_K activations): quantize the
+attention input, GEMV q (4096x4096), k, v (1024x4096); quantize the attention output, GEMV o
+(4096x4096); quantize the FFN input, GEMV gate, up (12288x4096, all Q4_K); quantize the FFN
+middle, GEMV down (4096x12288 Q6_K).  Weights are seeded N(0, 0.02) quantized by the repo's
+quantizer; the layer is resident in HBM in 32 copies at distinct addresses (3.9 GB) and step i
+uses copy i % 32, so the 256 MB Infinity Cache cannot serve repeats.  Steps are replayed from
+HIP graphs (one graph of 32 steps plus a remainder graph) so host launch overhead is not timed.
+
+value = algorithmic bytes per step (weights + activations read + outputs written, each once)
+        / measured time per step, in GB/s.
+Also reported: the dominant kernel's roofline fraction (Q4_K GEMV, per-launch HIP events), the
+reference CPU path (kc_matvec, fp32 activations) on the host cores, speculative-verify batched
+GEMV, the prefill GEMM and the full decode weight stream.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "oxcoder-9b_amd"))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "Q4_K decode GEMV GB/s (% of HBM peak) + prefill GEMM TOPS at 9B shapes"
+
+LAYER = [  # name, R, C, type, input slot
+    ("attn_q", 4096, 4096, 12, 0), ("attn_k", 1024, 4096, 12, 0), ("attn_v", 1024, 4096, 12, 0),
+    ("attn_output", 4096, 4096, 12, 1), ("ffn_gate", 12288, 4096, 12, 2), ("ffn_up", 12288, 4096, 12, 2),
+    ("ffn_down", 4096, 12288, 14, 3),
+]
+INPUT_COLS = [4096, 4096, 4096, 12288]
+BLOCK = {12: 144, 14: 210}
+Q8K = 292
+
+
+def wbytes(R, C_, ty):
+    return R * (C_ // 256) * BLOCK[ty]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Runner:
+    """Direct C-ABI launches with precomputed arguments (no per-call Python checks)."""
+
+    def __init__(self, torch):
+        from kq import _lib
+        self.torch = torch
+        self.lib = _lib.kq()
+        self.check = _lib.check
+
+    def stream(self):
+        return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+
+    def quantize(self, x, C_, xq, s):
+        self.check(self.lib.kq_q8k_quantize(C.c_void_p(x.data_ptr()), C_, C_, 1, C.c_void_p(xq.data_ptr()), s))
+
+    def gemv(self, w, R, C_, ty, xq, N, y, s):
+        self.check(self.lib.kq_gemv_q8k(C.c_void_p(w.data_ptr()), R, C_, ty, C.c_void_p(xq.data_ptr()), N,
+                                        C.c_void_p(y.data_ptr()), R, s))
+
+    def gemm(self, w, R, C_, ty, xq, M, y, s):
+        self.check(self.lib.kq_gemm_q8k(C.c_void_p(w.data_ptr()), R, C_, ty, C.c_void_p(xq.data_ptr()), M,
+                                        C.c_void_p(y.data_ptr()), R, s))
+
+
+def make_layer(torch, dev, copies):
+    from kq import quantize as kqq
+    base = {}
+    for i, (name, R, C_, ty, _) in enumerate(LAYER):
+        base[name] = torch.from_numpy(kqq.synthetic_matrix(R, C_, ty, seed=i)).to(dev)
+    layers = [base]
+    for _ in range(copies - 1):
+        layers.append({k: v.clone() for k, v in base.items()})
+    return layers
+
+
+def step_bytes():
+    """Algorithmic bytes of one decode-layer step."""
+    total = 0
+    for _, R, C_, ty, _ in LAYER:
+        total += wbytes(R, C_, ty) + (C_ // 256) * Q8K + R * 4
+    for C_ in INPUT_COLS:
+        total += C_ * 4 + (C_ // 256) * Q8K
+    return total
+
+
+def run_step(rn, layer, xs, xqs, ys, s):
+    for slot, C_ in enumerate(INPUT_COLS):
+        rn.quantize(xs[slot], C_, xqs[slot], s)
+        for name, R, C2, ty, sl in LAYER:
+            if sl == slot:
+                rn.gemv(layer[name], R, C2, ty, xqs[slot], 1, ys[name], s)
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()                      # warm the stream once outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graphs(torch, plan):
+    """plan: list of graphs to replay in order; returns elapsed seconds between events."""
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for g in plan:
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3
+
+
+def kernel_roofline(torch, rn, layers, xqs, ys, repeats=3):
+    """Per-launch HIP events around every Q4_K GEMV launch (the dominant kernel) on the launch
+    stream; returns (avg bytes per launch, avg seconds per launch, launches)."""
+    s = rn.stream()
+    pairs, nbytes = [], []
+    for _ in range(repeats):
+        for layer in layers:
+            for name, R, C_, ty, slot in LAYER:
+                if ty != 12:
+                    continue
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                rn.gemv(layer[name], R, C_, ty, xqs[slot], 1, ys[name], s)
+                b.record()
+                pairs.append((a, b))
+                nbytes.append(wbytes(R, C_, ty) + (C_ // 256) * Q8K + R * 4)
+    torch.cuda.synchronize()
+    secs = [a.elapsed_time(b) / 1e3 for a, b in pairs]
+    return float(np.mean(nbytes)), float(np.mean(secs)), len(secs)
+
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's CPU path (kc_matvec, fp32 activations) on the same layer shapes."""
+    from kq import quantize as kqq
+    from oracle import oracle
+    threads = int(os.environ.get("KQ_CPU_THREADS", os.environ.get("OMP_NUM_THREADS", "16")))
+    # libgomp has already read OMP_NUM_THREADS (the host quantizer uses it); set the team size
+    # of this thread's parallel regions through the runtime instead.
+    C.CDLL("libgomp.so.1").omp_set_num_threads(threads)
+    kind = "reference" if oracle.ref_available() else "port"
+    mats = []
+    for i, (name, R, C_, ty, slot) in enumerate(LAYER):
+        W = kqq.synthetic_matrix(R, C_, ty, seed=i)
+        mats.append((W, R, C_, ty, kqq.synthetic_activations(1, C_, seed=slot)[0]))
+    copies = [mats] + [[(W.copy(), R, C_, ty, x) for (W, R, C_, ty, x) in mats] for _ in range(3)]
+    fn = oracle.ref_matvec if kind == "reference" else oracle.matvec_f32
+    per_step = sum(wbytes(R, C_, ty) + C_ * 4 + R * 4 for (_, R, C_, ty, _) in mats)
+    for (W, R, C_, ty, x) in copies[0]:
+        fn(W, R, C_, ty, x)           # warm-up
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        for (W, R, C_, ty, x) in copies[n % len(copies)]:
+            fn(W, R, C_, ty, x)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": round(per_step * n / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": "%d decode-layer steps (7 matvecs, fp32 activations, kc_matvec%s) rotating 4 "
+                      "host copies (486 MB), %.1f s" % (n, "" if kind == "reference" else " restated", el)}
+
+
+def batched_extra(torch, rn, dev, steps):
+    """Speculative-verify batched GEMV, N in {2,4,8,16}: 12288x4096 Q4_K and 4096x12288 Q6_K."""
+    from kq import ops, quantize as kqq
+    out = {}
+    for name, R, C_, ty in (("gate_12288x4096_q4k", 12288, 4096, 12), ("down_4096x12288_q6k", 4096, 12288, 14)):
+        base = torch.from_numpy(kqq.synthetic_matrix(R, C_, ty, seed=40 + ty)).to(dev)
+        ws = [base] + [base.clone() for _ in range(15)]           # 16 copies: > 450 MB
+        for N in (1, 2, 4, 8, 16):
+            X = torch.from_numpy(kqq.synthetic_activations(N, C_, seed=N)).to(dev)
+            xq = torch.empty(N * (C_ // 256) * Q8K, dtype=torch.uint8, device=dev)
+            ops.q8k_quantize(X, xq.view(N, -1))
+            y = torch.empty((N, R), device=dev)
+            g = capture(torch, lambda: [rn.gemv(w, R, C_, ty, xq, N, y, rn.stream()) for w in ws])
+            reps = max(1, steps // 16)
+            time_graphs(torch, [g])
+            el = time_graphs(torch, [g] * reps)
+            per = el / (reps * len(ws))
+            nbytes = wbytes(R, C_, ty) + N * (C_ // 256) * Q8K + N * R * 4
+            out["%s_N%d" % (name, N)] = {"us": round(per * 1e6, 2), "GB/s": round(nbytes / per / 1e9, 1),
+                                         "TOPS": round(2 * N * R * C_ / per / 1e12, 2)}
+    return out
+
+
+def gemm_extra(torch, rn, dev):
+    """Prefill GEMM: M in {512, 2048}; 12288x4096 Q4_K and 4096x12288 Q6_K."""
+    from kq import ops, quantize as kqq
+    out = {}
+    for name, R, C_, ty in (("gate_12288x4096_q4k", 12288, 4096, 12), ("down_4096x12288_q6k", 4096, 12288, 14)):
+        w = torch.from_numpy(kqq.synthetic_matrix(R, C_, ty, seed=60 + ty)).to(dev)
+        for M in (512, 2048):
+            X = torch.from_numpy(kqq.synthetic_activations(M, C_, seed=M)).to(dev)
+            xq = ops.q8k_quantize(X)
+            y = torch.empty((M, R), device=dev)
+            g = capture(torch, lambda: rn.gemm(w, R, C_, ty, xq, M, y, rn.stream()))
+            time_graphs(torch, [g])
+            reps = 3
+            el = time_graphs(torch, [g] * reps) / reps
+            out["%s_M%d" % (name, M)] = {"us": round(el * 1e6, 1), "TOPS": round(2 * M * R * C_ / el / 1e12, 2),
+                                         "frac_int8_peak": round(2 * M * R * C_ / el / 1e12 / INT8_PEAK_TOPS, 4)}
+    return out
+
+
+def decode_stream_extra(torch, rn, dev):
+    """Full 9B-shaped decode weight stream at batch 1: 32 layers (Q6_K attn_v and ffn_down on
+    even layers, Q4_K otherwise) + 151936x4096 Q6_K lm_head; one graph per token."""
+    from kq import ops, quantize as kqq
+    shapes = {}
+    for i, (name, R, C_, ty, slot) in enumerate(LAYER):
+        for t in (12, 14) if name in ("attn_v", "ffn_down") else (ty,):
+            shapes[(name, t)] = torch.from_numpy(kqq.synthetic_matrix(R, C_, t, seed=100 + 10 * i + t)).to(dev)
+    head = torch.from_numpy(kqq.synthetic_matrix(151936, 4096, 14, seed=999)).to(dev)
+    layers, total = [], 0
+    for l in range(32):
+        lay = {}
+        for name, R, C_, ty, slot in LAYER:
+            t = (14 if l % 2 == 0 else 12) if name in ("attn_v", "ffn_down") else ty
+            lay[name] = (shapes[(name, t)].clone(), R, C_, t, slot)
+            total += wbytes(R, C_, t)
+        layers.append(lay)
+    total += wbytes(151936, 4096, 14)
+    xs = [torch.from_numpy(kqq.synthetic_activations(1, c, seed=s)[0]).to(dev) for s, c in enumerate(INPUT_COLS)]
+    xqs = [torch.empty((c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
+    ys = {name: torch.empty(R, device=dev) for name, R, _, _, _ in LAYER}
+    logits = torch.empty(151936, device=dev)
+
+    def token():
+        s = rn.stream()
+        for lay in layers:
+            for slot, c in enumerate(INPUT_COLS):
+                rn.quantize(xs[slot], c, xqs[slot], s)
+                for name, (w, R, C_, t, sl) in lay.items():
+                    if sl == slot:
+                        rn.gemv(w, R, C_, t, xqs[slot], 1, ys[name], s)
+        rn.quantize(xs[0], 4096, xqs[0], s)
+        rn.gemv(head, 151936, 4096, 14, xqs[0], 1, logits, s)
+
+    g = capture(torch, token)
+    time_graphs(torch, [g])
+    reps = 10
+    el = time_graphs(torch, [g] * reps) / reps
+    del layers, shapes, head
+    return {"weight_bytes_per_token": total, "ms_per_token": round(el * 1e3, 4),
+            "tokens_per_s": round(1 / el, 1), "GB/s": round(total / el / 1e9, 1),
+            "hbm_frac": round(total / el / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=640)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--copies", type=int, default=32)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the products shard by "
+              "output rows with no exchange; see the design notes). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rn = Runner(torch)
+    log("bench: building %d resident layer copies" % a.copies)
+    layers = make_layer(torch, dev, a.copies)
+    from kq import quantize as kqq
+    xs = [torch.from_numpy(kqq.synthetic_activations(1, c, seed=s)[0]).to(dev) for s, c in enumerate(INPUT_COLS)]
+    xqs = [torch.empty((c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
+    ys = {name: torch.empty(R, device=dev) for name, R, _, _, _ in LAYER}
+
+    def steps(n, start=0):
+        def fn():
+            s = rn.stream()
+            for i in range(start, start + n):
+                run_step(rn, layers[i % a.copies], xs, xqs, ys, s)
+        return fn
+
+    full = capture(torch, steps(a.copies))
+    rem = a.steps % a.copies
+    tail = capture(torch, steps(rem)) if rem else None
+    plan = [full] * (a.steps // a.copies) + ([tail] if tail else [])
+    log("bench: warmup %d steps" % a.warmup)
+    time_graphs(torch, [full] * max(1, a.warmup // a.copies))
+    el = time_graphs(torch, plan)
+    per_step = el / a.steps
+    nbytes = step_bytes()
+    value = nbytes / per_step / 1e9
+    log("bench: %.2f us/step  %.1f GB/s" % (per_step * 1e6, value))
+
+    kb, ks, kn = kernel_roofline(torch, rn, layers, xqs, ys)
+    achieved = kb / ks / 1e9
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(per_step * 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,0.02) weights quantized by the repo quantizer; N(0,1) activations)",
+        "config": {"workload": "one 9B-class decode layer's projections at batch 1 with Q8_K activations: "
+                               "q/o 4096x4096, k/v 1024x4096, gate/up 12288x4096 Q4_K, down 4096x12288 Q6_K, "
+                               "plus 4 activation quantizations",
+                   "bytes_per_step": nbytes, "resident_layer_copies": a.copies,
+                   "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv_q4k_q8k (Q4_K x Q8_K GEMV)", "launches": kn,
+                     "avg_bytes_per_launch": round(kb), "avg_us_per_launch": round(ks * 1e6, 3)},
+    }
+    if not a.no_extras:
+        log("bench: batched GEMV")
+        result["batched_gemv"] = batched_extra(torch, rn, dev, 160)
+        log("bench: prefill GEMM")
+        result["prefill_gemm"] = gemm_extra(torch, rn, dev)
+        del layers
+        torch.cuda.empty_cache()
+        log("bench: full decode stream")
+        result["decode_stream"] = decode_stream_extra(torch, rn, dev)
+    if not a.no_cpu:
+        log("bench: CPU baseline")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

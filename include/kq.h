@@ -76,6 +76,14 @@ int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, fl
                 int64_t ldy, void* stream);
 
 /*
+ * Up to 3 matrices sharing one Q8_K input in one launch per type (q/k/v, gate/up): the Q8_K
+ * form of the CPU engine's multi-matrix gemv(m, n, A, y, x) (kcpu4.c:100-118).  C and N are
+ * common; R[i], type[i], y[i] and ldy[i] per matrix.
+ */
+int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const int* type, const void* xq,
+                      int N, float* const* y, const int64_t* ldy, void* stream);
+
+/*
  * Prefill GEMM: Y[m][r] for M >= 1 activation rows (row stride ldy), int8 products with int32
  * accumulation and the fp32 epilogue above.  Slot of the ternary engine's chunk GEMM
  * k_mm_g5q (chunk.cu:820) driven by chunk.feed (chunk.py:378); the Q4 engine itself prefills

@@ -100,10 +100,43 @@ int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, fl
     KQ_TRY(check_matrix(w, R, C, type, fn));
     if (N < 1 || N > KQ_MAX_BATCH) return fail(KQ_ERR_ARG, "%s: N=%d must be 1..%d", fn, N, KQ_MAX_BATCH);
     if (N > 1 && ldy < R) return fail(KQ_ERR_ARG, "%s: ldy=%lld is smaller than R=%d", fn, (long long)ldy, R);
+    if (R / 8 > (1 << 27)) return fail(KQ_ERR_ARG, "%s: R=%d too large for one call", fn, R);
     KQ_TRY(check_ptr(xq, 4, "xq", fn));
     KQ_TRY(check_ptr(y, 4, "y", fn));
     launch_gemv_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), N, y,
                     ldy, 0, as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const int* type, const void* xq,
+                      int N, float* const* y, const int64_t* ldy, void* stream) {
+    static const char* fn = "kq_gemv_q8k_multi";
+    if (n < 1 || n > 3) return fail(KQ_ERR_ARG, "%s: n=%d must be 1..3", fn, n);
+    if (!w || !R || !type || !y || !ldy) return fail(KQ_ERR_ARG, "%s: NULL array argument", fn);
+    if (N < 1 || N > KQ_MAX_BATCH) return fail(KQ_ERR_ARG, "%s: N=%d must be 1..%d", fn, N, KQ_MAX_BATCH);
+    int64_t tiles = 0;
+    for (int i = 0; i < n; i++) {
+        KQ_TRY(check_matrix(w[i], R[i], C, type[i], fn));
+        KQ_TRY(check_ptr(y[i], 4, "y[i]", fn));
+        if (N > 1 && ldy[i] < R[i]) return fail(KQ_ERR_ARG, "%s: ldy[%d] is smaller than R", fn, i);
+        tiles += R[i] / 8;
+    }
+    if (tiles > (1 << 27)) return fail(KQ_ERR_ARG, "%s: too many rows in one call", fn);
+    KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    // matrices of the same type share a launch
+    for (int ty : {KQ_TYPE_Q4_K, KQ_TYPE_Q6_K}) {
+        const uint8_t* ws[3];
+        int rs[3];
+        float* ys[3];
+        int64_t ls[3];
+        int k = 0;
+        for (int i = 0; i < n; i++)
+            if (type[i] == ty) {
+                ws[k] = static_cast<const uint8_t*>(w[i]); rs[k] = R[i]; ys[k] = y[i]; ls[k] = N > 1 ? ldy[i] : R[i];
+                k++;
+            }
+        if (k) launch_gemv_q8k_group(k, ws, rs, C, ty, static_cast<const uint8_t*>(xq), N, ys, ls, as_stream(stream));
+    }
     return check_launch(fn);
 }
 

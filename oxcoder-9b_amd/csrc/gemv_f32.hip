@@ -139,9 +139,9 @@ k_gemv_q6k_f32(const uint8_t* __restrict__ W, const float* __restrict__ X, float
                 const u32x4 l1 = ld16_a2(bk + h * 64 + 32 + 16 * jj);
                 const u32x4 hb = ld16_a2(bk + 128 + h * 32 + 16 * jj);
                 const u32x4 s = ld16_a2(bk + 192);
-                const uintptr_t da = reinterpret_cast<uintptr_t>(bk + 208);
-                const uint32_t dw = ld4(reinterpret_cast<const uint8_t*>(da & ~uintptr_t(3)));
-                const float d = f16_lo(dw >> (8 * (da & 3)));
+                const uint32_t dsh = uint32_t(reinterpret_cast<uintptr_t>(bk) & 3);
+                const uint32_t dw = ld4(bk + 208 - dsh);
+                const float d = f16_lo(dw >> (8 * dsh));
                 const uint32_t w0 = h ? s.z : s.x, w1 = h ? s.w : s.y;
                 const int sc[4] = {sbyte(w0, jj), sbyte(w0, jj + 2), sbyte(w1, jj), sbyte(w1, jj + 2)};
                 const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};

@@ -1,254 +1,481 @@
 // Q4_K / Q6_K x Q8_K GEMV for gfx950 (batch-1 decode and small-batch speculative verify).
 //
-// Work split: one wave owns RPW consecutive rows of one 8-row tile; the wave walks the
-// super-block columns 16 at a time (slot = lane >> 2, g = slot + 16*pass) with four lanes per
-// super-block.  Each lane streams its share of every tile column with 16-byte loads (a Q4_K tile
-// column is 1152 B = 9 cache lines, read once), keeps the RPW rows' quants in registers and runs
-// them against each token's Q8_K activations with v_dot4_i32_i8.  Per (row, super-block) the four
-// lanes' int32 partials are summed exactly (quad shuffle), turned into one fp32 value, and the
-// values are reduced by the pairwise column tree of q4_lanes.h.  HBM traffic per call is the
-// weight bytes once plus activations and outputs; activations are re-read from L1/L2 per row group.
+// Work unit: RPW consecutive rows of one 8-row tile of one matrix.  Up to three matrices that
+// share the activation (q/k/v, gate/up) are one launch: their units are numbered back to back.
+// The grid is sized to the chip (KQ_GEMV_WAVES_PER_CU waves per CU, fewer if there are fewer
+// units) and each wave walks units u = wave, wave + nwaves, ...; while it computes one
+// (unit, column pass) it already has the loads of the next one in flight, so weight streaming
+// and the dot/reduce work of a wave overlap instead of alternating.
+//
+// Lanes: slot = lane >> 2 walks super-block columns g = slot + 16*pass, part = lane & 3 owns a
+// quarter of the super-block (q4_lanes.h).  Per row a Q4_K lane reads the 16-B block header and
+// 32 quant bytes (a tile column is 9 cache lines, each read once); a Q6_K lane reads 48 quant
+// bytes plus scales and d with dword-aligned funnel-shifted loads.  Per (row, super-block) the
+// four lanes' int32 partials are summed exactly, turned into one fp32 value and reduced by the
+// column tree of q4_lanes.h, so the result does not depend on NT, RPW or grid shape.
 #include "kq_device.h"
 #include "kq_internal.h"
 #include "q4_lanes.h"
 
+#ifndef KQ_GEMV_WAVES_PER_CU
+#define KQ_GEMV_WAVES_PER_CU 8
+#endif
+#ifndef KQ_GEMV_WG_WAVES
+#define KQ_GEMV_WG_WAVES 4
+#endif
+#ifndef KQ_GEMV_BLOCKED
+#define KQ_GEMV_BLOCKED 0  // 1: contiguous unit ranges per stream, streams grouped per XCD
+#endif
+#ifndef KQ_XCDS
+#define KQ_XCDS 8          // accelerator complex dies per MI355X; workgroups alternate between them
+#endif
+
 namespace kq {
 
-// ----------------------------------------------------------------------------- Q4_K
-template <int NT, int RPW>
-__global__ void __launch_bounds__(256)
-k_gemv_q4k_q8k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ, float* __restrict__ Y,
-               int R, int G, int64_t ldy) {
-    constexpr int WPT = 8 / RPW;  // waves per 8-row tile
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int64_t tile = wave / WPT;
-    if (tile >= R / 8) return;
-    const int r0 = (int)(wave - tile * WPT) * RPW;
-    const int p = lane & 3, slot = lane >> 2;
-    const uint8_t* Wt = W + tile * (int64_t)G * (8 * Q4K_BYTES) + r0 * Q4K_BYTES;
+struct MatGroup {
+    const uint8_t* w[3];
+    float* y[3];
+    int64_t ldy[3];
+    int first_unit[4];   // units of matrix m are [first_unit[m], first_unit[m+1])
+    int n;
+};
 
-    PassTree tree[NT][RPW];
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < RPW; r++) tree_init(tree[t][r]);
+// ------------------------------------------------------------------ per-type fragments
+template <int TYPE> struct Frag;
+template <> struct Frag<TYPE_Q4_K> { u32x4 hdr, qa, qb; };
+// Q6_K fields sit at block offset + (block start & 3): the fragment holds the raw dword-aligned
+// words (each 16-B field + the following dword) and the byte shift; the funnel shift happens in
+// block_value so that issuing a prefetch never waits for its data.
+template <> struct Frag<TYPE_Q6_K> { u32x4 l0, l1, hb; uint32_t l0e, l1e, hbe; u32x2 sc; uint32_t sce, dw, sh; };
 
-    const int passes = (G + 15) >> 4;
-    for (int pass = 0; pass < passes; pass++) {
-        const int g = slot + 16 * pass;
-        const bool valid = g < G;
-        u32x4 hdr[RPW], qa[RPW], qb[RPW];
-        if (valid) {
-#pragma unroll
-            for (int r = 0; r < RPW; r++) {
-                const uint8_t* bk = Wt + (int64_t)g * (8 * Q4K_BYTES) + r * Q4K_BYTES;
-                hdr[r] = ld16(bk);
-                qa[r] = ld16(bk + 16 + 32 * p);
-                qb[r] = ld16(bk + 32 + 32 * p);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < RPW; r++) hdr[r] = qa[r] = qb[r] = u32x4{0, 0, 0, 0};
-        }
-        ScMin sm[RPW];
-#pragma unroll
-        for (int r = 0; r < RPW; r++) sm[r] = q4k_scmin_pair(hdr[r].y, hdr[r].z, hdr[r].w, p);
+template <int TYPE> struct Act;
+template <> struct Act<TYPE_Q4_K> { uint32_t xl[8], xh[8]; int blo, bhi; float dx; };
+template <> struct Act<TYPE_Q6_K> { uint32_t xa[16]; int corr[4]; float dx; };
 
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            uint32_t xl[8], xh[8];
-            float dx = 0.0f;
-            int blo = 0, bhi = 0;
-            if (valid) {
-                const uint8_t* xb = XQ + ((int64_t)t * G + g) * Q8K_BYTES;
-                dx = __builtin_bit_cast(float, ld4(xb));
-                const u32x4 a0 = ld16_a4(xb + 4 + 64 * p), a1 = ld16_a4(xb + 20 + 64 * p);
-                const u32x4 a2 = ld16_a4(xb + 36 + 64 * p), a3 = ld16_a4(xb + 52 + 64 * p);
-                xl[0] = a0.x; xl[1] = a0.y; xl[2] = a0.z; xl[3] = a0.w;
-                xl[4] = a1.x; xl[5] = a1.y; xl[6] = a1.z; xl[7] = a1.w;
-                xh[0] = a2.x; xh[1] = a2.y; xh[2] = a2.z; xh[3] = a2.w;
-                xh[4] = a3.x; xh[5] = a3.y; xh[6] = a3.z; xh[7] = a3.w;
-                const uint32_t b01 = ld4(xb + 260 + 8 * p), b23 = ld4(xb + 264 + 8 * p);
-                blo = shalf(b01, 0) + shalf(b01, 1);
-                bhi = shalf(b23, 0) + shalf(b23, 1);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 8; k++) xl[k] = xh[k] = 0;
-            }
-#pragma unroll
-            for (int r = 0; r < RPW; r++) {
-                int plo, phi;
-                q4k_lane_dots(qa[r], qb[r], xl, xh, plo, phi);
-                const int i1 = quad_sum_i32((int)sm[r].sc_lo * plo + (int)sm[r].sc_hi * phi);
-                const int i2 = quad_sum_i32((int)sm[r].m_lo * blo + (int)sm[r].m_hi * bhi);
-                const float v = valid ? q4k_value(hdr[r].x, dx, i1, i2) : 0.0f;
-                tree_push(tree[t][r], slot_tree_f32(v));
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            const float y = tree_final(tree[t][r]);
-            if (lane == 0) Y[(int64_t)t * ldy + tile * 8 + r0 + r] = y;
-        }
+// bk = first byte of this row's block; p = part.
+__device__ __forceinline__ void load_frag(Frag<TYPE_Q4_K>& f, const uint8_t* bk, int p) {
+    f.hdr = ld16(bk);
+    f.qa = ld16(bk + 16 + 32 * p);
+    f.qb = ld16(bk + 32 + 32 * p);
 }
-
-// ----------------------------------------------------------------------------- Q6_K
-// Block bytes of row r start at an offset = 2r (mod 16) inside a 16-byte aligned tile column,
-// so the lane fields (16 B each) are read with dword-aligned loads plus a funnel shift.  Every
-// such read stays inside the 8-row tile column: the last field of a block ends at byte 192 and
-// the scale/d window [192, 210) is read from the dword containing byte 192 or 190.
-template <int NT, int RPW>
-__global__ void __launch_bounds__(256)
-k_gemv_q6k_q8k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ, float* __restrict__ Y,
-               int R, int G, int64_t ldy) {
-    constexpr int WPT = 8 / RPW;
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int64_t tile = wave / WPT;
-    if (tile >= R / 8) return;
-    const int r0 = (int)(wave - tile * WPT) * RPW;
-    const int p = lane & 3, slot = lane >> 2;
+// Q6_K reads stay inside the row's 8-row tile column: quant fields end at byte 192 of the block,
+// the scale window [192 + 8h, 200 + 8h) and d [208, 210) are read from the dword-aligned address
+// at or below them; for even rows (block start = 0 mod 4) the last word read reaches 2 bytes
+// into the next row's block, which exists because row 7 of a tile is odd.
+__device__ __forceinline__ void load_frag(Frag<TYPE_Q6_K>& f, const uint8_t* bk, int p) {
     const int h = p >> 1, jj = p & 1;
-    const uint8_t* Wt = W + tile * (int64_t)G * (8 * Q6K_BYTES) + r0 * Q6K_BYTES;
+    // pointer arithmetic (not an integer round trip) keeps the global address space
+    f.sh = uint32_t(reinterpret_cast<uintptr_t>(bk) & 3);   // the same shift for every field
+    const uint8_t* b4 = bk - f.sh;
+    f.l0 = ld16_a4(b4 + h * 64 + 16 * jj);
+    f.l0e = ld4(b4 + h * 64 + 16 * jj + 16);
+    f.l1 = ld16_a4(b4 + h * 64 + 32 + 16 * jj);
+    f.l1e = ld4(b4 + h * 64 + 32 + 16 * jj + 16);
+    f.hb = ld16_a4(b4 + 128 + h * 32 + 16 * jj);
+    f.hbe = ld4(b4 + 128 + h * 32 + 16 * jj + 16);
+    f.sc = *reinterpret_cast<const u32x2_a4*>(b4 + 192 + 8 * h);
+    f.sce = ld4(b4 + 200 + 8 * h);
+    f.dw = ld4(b4 + 208);
+}
+__device__ __forceinline__ u32x4 funnel(const u32x4& v, uint32_t e, uint32_t sh) {
+    u32x4 r;
+    r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    r.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    r.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
+    return r;
+}
 
+// xb = first byte of the Q8_K block of column g for one token.
+__device__ __forceinline__ void load_act(Act<TYPE_Q4_K>& a, const uint8_t* xb, int p) {
+    a.dx = __builtin_bit_cast(float, ld4(xb));
+    const u32x4 a0 = ld16_a4(xb + 4 + 64 * p), a1 = ld16_a4(xb + 20 + 64 * p);
+    const u32x4 a2 = ld16_a4(xb + 36 + 64 * p), a3 = ld16_a4(xb + 52 + 64 * p);
+    a.xl[0] = a0.x; a.xl[1] = a0.y; a.xl[2] = a0.z; a.xl[3] = a0.w;
+    a.xl[4] = a1.x; a.xl[5] = a1.y; a.xl[6] = a1.z; a.xl[7] = a1.w;
+    a.xh[0] = a2.x; a.xh[1] = a2.y; a.xh[2] = a2.z; a.xh[3] = a2.w;
+    a.xh[4] = a3.x; a.xh[5] = a3.y; a.xh[6] = a3.z; a.xh[7] = a3.w;
+    const uint32_t b01 = ld4(xb + 260 + 8 * p), b23 = ld4(xb + 264 + 8 * p);
+    a.blo = shalf(b01, 0) + shalf(b01, 1);
+    a.bhi = shalf(b23, 0) + shalf(b23, 1);
+}
+__device__ __forceinline__ void load_act(Act<TYPE_Q6_K>& a, const uint8_t* xb, int p) {
+    const int h = p >> 1, jj = p & 1;
+    a.dx = __builtin_bit_cast(float, ld4(xb));
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const u32x4 v = ld16_a4(xb + 4 + h * 128 + k * 32 + 16 * jj);
+        a.xa[4 * k + 0] = v.x; a.xa[4 * k + 1] = v.y; a.xa[4 * k + 2] = v.z; a.xa[4 * k + 3] = v.w;
+    }
+    const u32x4 bs = ld16_a4(xb + 260 + 16 * h);   // bsums 8h..8h+7; sub-block 8h+2k+jj = dword k, half jj
+    a.corr[0] = 32 * shalf(bs.x, jj);
+    a.corr[1] = 32 * shalf(bs.y, jj);
+    a.corr[2] = 32 * shalf(bs.z, jj);
+    a.corr[3] = 32 * shalf(bs.w, jj);
+}
+// Super-block value of one row for one token (same in all four lanes of the quad).
+__device__ __forceinline__ float block_value(const Frag<TYPE_Q4_K>& f, const Act<TYPE_Q4_K>& a, int p) {
+    const ScMin sm = q4k_scmin_pair(f.hdr.y, f.hdr.z, f.hdr.w, p);
+    int plo, phi;
+    q4k_lane_dots(f.qa, f.qb, a.xl, a.xh, plo, phi);
+    const int i1 = quad_sum_i32((int)sm.sc_lo * plo + (int)sm.sc_hi * phi);
+    const int i2 = quad_sum_i32((int)sm.m_lo * a.blo + (int)sm.m_hi * a.bhi);
+    return q4k_value(f.hdr.x, a.dx, i1, i2);
+}
+__device__ __forceinline__ float block_value(const Frag<TYPE_Q6_K>& f, const Act<TYPE_Q6_K>& a, int p) {
+    const int jj = p & 1;
+    const uint32_t w0 = __builtin_amdgcn_alignbyte(f.sc.y, f.sc.x, f.sh);   // scales 8h .. 8h+3
+    const uint32_t w1 = __builtin_amdgcn_alignbyte(f.sce, f.sc.y, f.sh);    // scales 8h+4 .. 8h+7
+    int P[4];
+    q6k_lane_dots(funnel(f.l0, f.l0e, f.sh), funnel(f.l1, f.l1e, f.sh), funnel(f.hb, f.hbe, f.sh), a.xa, P);
+    int I = sbyte(w0, jj) * (P[0] - a.corr[0]);
+    I += sbyte(w0, jj + 2) * (P[1] - a.corr[1]);
+    I += sbyte(w1, jj) * (P[2] - a.corr[2]);
+    I += sbyte(w1, jj + 2) * (P[3] - a.corr[3]);
+    I = quad_sum_i32(I);
+    return q6k_value(f16_lo(f.dw >> (8 * f.sh)), a.dx, I);
+}
+
+// ------------------------------------------------------------------ the kernel
+template <int TYPE, int NT, int RPW, bool ONEPASS>
+__global__ void __launch_bounds__(256)
+k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) {
+    constexpr int WPT = 8 / RPW;
+    constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    const int lane = threadIdx.x & 63;
+    const int nwaves = gridDim.x * (blockDim.x >> 6);
+    // Unit bookkeeping is wave-uniform: readfirstlane keeps it in scalar registers.
+    int u = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (u >= total_units) return;
+    const int p = lane & 3, slot = lane >> 2;
+    const int passes = ONEPASS ? 1 : (G + 15) >> 4;
+    const int64_t col_bytes = 8 * BS;                  // one tile column
+    const int64_t tile_bytes = (int64_t)G * col_bytes;
+
+    // Unit -> (matrix, first row) and the row-block address.  The unit index is wave-uniform,
+    // so the argument-struct reads below are scalar loads and never wait on the weight stream.
+    auto unit_base = [&](int uu, int& m, int64_t& row0) -> const uint8_t* {
+        m = uu >= mg.first_unit[1] ? (uu >= mg.first_unit[2] ? 2 : 1) : 0;
+        const int v = uu - mg.first_unit[m];
+        const int64_t tile = v / WPT;
+        const int r0 = (v - (int)tile * WPT) * RPW;
+        row0 = tile * 8 + r0;
+        return mg.w[m] + tile * tile_bytes + r0 * BS;
+    };
+
+    // Every load below is unconditional (lanes past the last column read column G-1 and their
+    // values are masked to zero), so the number of loads in flight is static and the compiler
+    // can wait for the current step's data without draining the next step's prefetch.
+    const int slot_c = slot < G ? slot : G - 1;
+    Act<TYPE> act[NT];
+    if (ONEPASS) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) load_act(act[t], XQ + ((int64_t)t * G + slot_c) * Q8K_BYTES, p);
+    }
+
+    Frag<TYPE> bufA[RPW], bufB[RPW];
+    int m;
+    int64_t row0;
+    const uint8_t* base = unit_base(u, m, row0);
+#pragma unroll
+    for (int r = 0; r < RPW; r++) load_frag(bufA[r], base + (int64_t)slot_c * col_bytes + r * BS, p);
     PassTree tree[NT][RPW];
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int r = 0; r < RPW; r++) tree_init(tree[t][r]);
 
-    const int passes = (G + 15) >> 4;
-    for (int pass = 0; pass < passes; pass++) {
+    int pass = 0;
+    // One (unit, pass) step: issue the next step's loads into `nxt`, then compute from `cur`.
+    // The loop body runs two steps with the buffers swapped, so no register copy (which would
+    // have to wait for the prefetch) is needed.  The last step re-reads its own unit so the
+    // number of loads in flight stays fixed.
+    auto step = [&](Frag<TYPE>* cur, Frag<TYPE>* nxt) -> bool {
+        int un = u, pn = pass + 1;
+        if (pn == passes) { pn = 0; un = u + nwaves; }
+        const bool has_next = un < total_units;
+        int mn = m;
+        int64_t row0n = row0;
+        const uint8_t* basen = base;
+        if (has_next && un != u) basen = unit_base(un, mn, row0n);
+        {
+            int gn = slot + 16 * (has_next ? pn : pass);
+            gn = gn < G ? gn : G - 1;
+#pragma unroll
+            for (int r = 0; r < RPW; r++) load_frag(nxt[r], basen + (int64_t)gn * col_bytes + r * BS, p);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
         const int g = slot + 16 * pass;
         const bool valid = g < G;
-        u32x4 l0[RPW], l1[RPW], hb[RPW];
-        int sc[RPW][4];
-        float d[RPW];
-        if (valid) {
+        if (!ONEPASS) {
+            const int gc = valid ? g : G - 1;
 #pragma unroll
-            for (int r = 0; r < RPW; r++) {
-                const uint8_t* bk = Wt + (int64_t)g * (8 * Q6K_BYTES) + r * Q6K_BYTES;
-                l0[r] = ld16_a2(bk + h * 64 + 16 * jj);
-                l1[r] = ld16_a2(bk + h * 64 + 32 + 16 * jj);
-                hb[r] = ld16_a2(bk + 128 + h * 32 + 16 * jj);
-                const u32x4 s = ld16_a2(bk + 192);       // 16 int8 scales
-                const uintptr_t da = reinterpret_cast<uintptr_t>(bk + 208);
-                const uint32_t dw = ld4(reinterpret_cast<const uint8_t*>(da & ~uintptr_t(3)));
-                d[r] = f16_lo(dw >> (8 * (da & 3)));
-                const uint32_t w0 = h ? s.z : s.x, w1 = h ? s.w : s.y;   // scales 8h .. 8h+7
-                sc[r][0] = sbyte(w0, jj);
-                sc[r][1] = sbyte(w0, jj + 2);
-                sc[r][2] = sbyte(w1, jj);
-                sc[r][3] = sbyte(w1, jj + 2);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < RPW; r++) {
-                l0[r] = l1[r] = hb[r] = u32x4{0, 0, 0, 0};
-                sc[r][0] = sc[r][1] = sc[r][2] = sc[r][3] = 0;
-                d[r] = 0.0f;
-            }
+            for (int t = 0; t < NT; t++) load_act(act[t], XQ + ((int64_t)t * G + gc) * Q8K_BYTES, p);
         }
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            uint32_t xa[16];
-            int corr[4];
-            float dx = 0.0f;
-            if (valid) {
-                const uint8_t* xb = XQ + ((int64_t)t * G + g) * Q8K_BYTES;
-                dx = __builtin_bit_cast(float, ld4(xb));
+        for (int t = 0; t < NT; t++)
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const u32x4 a = ld16_a4(xb + 4 + h * 128 + k * 32 + 16 * jj);
-                    xa[4 * k + 0] = a.x; xa[4 * k + 1] = a.y; xa[4 * k + 2] = a.z; xa[4 * k + 3] = a.w;
+            for (int r = 0; r < RPW; r++) {
+                const float v = block_value(cur[r], act[t], p);
+                tree_push(tree[t][r], slot_tree_f32(valid ? v : 0.0f));
+            }
+
+        if (pass == passes - 1) {
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int r = 0; r < RPW; r++) {
+                    const float y = tree_final(tree[t][r]);
+                    if (lane == 0) mg.y[m][t * mg.ldy[m] + row0 + r] = y;
+                    tree_init(tree[t][r]);
                 }
-                // bsums of sub-blocks 8h + 2k + jj, k = 0..3 (dword k of bsums[8h..8h+7])
-                const u32x4 bs = ld16_a4(xb + 260 + 16 * h);
-                corr[0] = 32 * shalf(bs.x, jj);
-                corr[1] = 32 * shalf(bs.y, jj);
-                corr[2] = 32 * shalf(bs.z, jj);
-                corr[3] = 32 * shalf(bs.w, jj);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 16; k++) xa[k] = 0;
-                corr[0] = corr[1] = corr[2] = corr[3] = 0;
-            }
-#pragma unroll
-            for (int r = 0; r < RPW; r++) {
-                int P[4];
-                q6k_lane_dots(l0[r], l1[r], hb[r], xa, P);
-                int I = sc[r][0] * (P[0] - corr[0]);
-                I += sc[r][1] * (P[1] - corr[1]);
-                I += sc[r][2] * (P[2] - corr[2]);
-                I += sc[r][3] * (P[3] - corr[3]);
-                I = quad_sum_i32(I);
-                const float v = valid ? q6k_value(d[r], dx, I) : 0.0f;
-                tree_push(tree[t][r], slot_tree_f32(v));
-            }
         }
+        if (!has_next) return false;
+        u = un; pass = pn; m = mn; row0 = row0n; base = basen;
+        return true;
+    };
+    while (step(bufA, bufB) && step(bufB, bufA)) {
     }
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            const float y = tree_final(tree[t][r]);
-            if (lane == 0) Y[(int64_t)t * ldy + tile * 8 + r0 + r] = y;
-        }
 }
 
-// ----------------------------------------------------------------------------- launch
-template <int NT, int RPW>
-static void launch_nt(const uint8_t* w, int R, int G, int type, const uint8_t* xq, float* y,
-                      int64_t ldy, hipStream_t s) {
-    const int64_t waves = (int64_t)(R / 8) * (8 / RPW);
+// ------------------------------------------------------------------ pass-split kernel
+// For C <= 16384 (at most 4 column passes).  A workgroup holds K unit streams of P waves each
+// (P = passes): wave (stream, pass) keeps the activations of its pass in registers and streams
+// that pass's tile columns for every unit of its stream (units s, s + nstreams, ...),
+// prefetching the next unit.  Each (unit, token, row) pass value goes to LDS; after one barrier
+// the workgroup merges them with the same pass tree as the sequential kernel and stores y.  With
+// one pass the value is stored directly.
+template <int TYPE, int NT, int RPW>
+__global__ void __launch_bounds__(256)
+k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units, int P, int kmax) {
+    constexpr int WPT = 8 / RPW;
+    constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    extern __shared__ float part[];                    // [stream][k][t][r][pass]
+    const int K = (blockDim.x >> 6) / P;               // unit streams per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int pass = wave % P, stream = wave / P;
+    // Workgroups are dispatched round-robin over the XCDs (8 on MI355X, each with its own L2);
+    // renumber them so that each XCD owns one contiguous range of streams, and give each stream
+    // a contiguous range of units: neighbouring rows (which share cache lines, since 144- and
+    // 210-byte blocks do not align to 128-byte lines) are then read through the same L2.
+    // (KQ_GEMV_BLOCKED=0 keeps dispatch order and interleaves units over streams instead.)
+    const int nwg = gridDim.x;                         // a multiple of KQ_XCDS
+#if KQ_GEMV_BLOCKED
+    const int lwg = (blockIdx.x % KQ_XCDS) * (nwg / KQ_XCDS) + blockIdx.x / KQ_XCDS;
+#else
+    const int lwg = blockIdx.x;
+#endif
+    const int sid = lwg * K + stream, nstreams = nwg * K;
+#if KQ_GEMV_BLOCKED
+    const int per = (total_units + nstreams - 1) / nstreams;
+    const int u_begin = sid * per, u_step = 1;
+    const int u_end = u_begin + per < total_units ? u_begin + per : total_units;
+#else
+    const int u_begin = sid, u_step = nstreams, u_end = total_units;
+#endif
+    const int p = lane & 3, slot = lane >> 2;
+    const int64_t col_bytes = 8 * BS;
+    const int64_t tile_bytes = (int64_t)G * col_bytes;
+    const int g = slot + 16 * pass;
+    const bool valid = g < G;
+    const int gc = valid ? g : G - 1;                  // lanes past the last column read column G-1, masked
+
+    auto unit_base = [&](int uu, int& m, int64_t& row0) -> const uint8_t* {
+        m = uu >= mg.first_unit[1] ? (uu >= mg.first_unit[2] ? 2 : 1) : 0;
+        const int v = uu - mg.first_unit[m];
+        const int64_t tile = v / WPT;
+        const int r0 = (v - (int)tile * WPT) * RPW;
+        row0 = tile * 8 + r0;
+        return mg.w[m] + tile * tile_bytes + r0 * BS + gc * col_bytes;
+    };
+
+    if (u_begin < u_end) {
+        Act<TYPE> act[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) load_act(act[t], XQ + ((int64_t)t * G + gc) * Q8K_BYTES, p);
+
+        Frag<TYPE> bufA[RPW], bufB[RPW];
+        int u = u_begin, k = 0, m;
+        int64_t row0;
+        const uint8_t* base = unit_base(u, m, row0);
+#pragma unroll
+        for (int r = 0; r < RPW; r++) load_frag(bufA[r], base + r * BS, p);
+        float* mypart = part + (int64_t)stream * kmax * NT * RPW * P;
+
+        auto step = [&](Frag<TYPE>* cur, Frag<TYPE>* nxt) -> bool {
+            const int un = u + u_step;
+            const bool has_next = un < u_end;
+            int mn = m;
+            int64_t row0n = row0;
+            const uint8_t* basen = has_next ? unit_base(un, mn, row0n) : base;
+#pragma unroll
+            for (int r = 0; r < RPW; r++) load_frag(nxt[r], basen + r * BS, p);
+            // keep every prefetch load ahead of this step's compute (and its waits)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int r = 0; r < RPW; r++) {
+                    const float v = block_value(cur[r], act[t], p);
+                    const float pv = slot_tree_f32(valid ? v : 0.0f);
+                    if (P == 1) {
+                        if (lane == 0) mg.y[m][t * mg.ldy[m] + row0 + r] = __fadd_rn(pv, 0.0f);
+                    } else if (lane == 0) {
+                        mypart[((k * NT + t) * RPW + r) * P + pass] = pv;
+                    }
+                }
+            if (!has_next) return false;
+            u = un; k++; m = mn; row0 = row0n; base = basen;
+            return true;
+        };
+        while (step(bufA, bufB) && step(bufB, bufA)) {
+        }
+    }
+    if (P == 1) return;
+
+    __syncthreads();
+    for (int st = 0; st < K; st++) {
+        const int s0 = lwg * K + st;
+#if KQ_GEMV_BLOCKED
+        const int per = (total_units + nstreams - 1) / nstreams;
+        const int b0 = s0 * per, bstep = 1;
+        const int nk = b0 < total_units ? (b0 + per < total_units ? per : total_units - b0) : 0;
+#else
+        const int b0 = s0, bstep = nstreams;
+        const int nk = b0 < total_units ? (total_units - b0 + nstreams - 1) / nstreams : 0;
+#endif
+        const float* sp = part + (int64_t)st * kmax * NT * RPW * P;
+        for (int idx = threadIdx.x; idx < nk * NT * RPW; idx += blockDim.x) {
+            const int kk = idx / (NT * RPW), t = (idx / RPW) % NT, r = idx % RPW;
+            const int uu = b0 + kk * bstep;
+            const int mm = uu >= mg.first_unit[1] ? (uu >= mg.first_unit[2] ? 2 : 1) : 0;
+            const int v = uu - mg.first_unit[mm];
+            const int64_t rowr = (int64_t)(v / WPT) * 8 + (v % WPT) * RPW + r;
+            PassTree tr;
+            tree_init(tr);
+            for (int q = 0; q < P; q++) tree_push(tr, sp[idx * P + q]);
+            mg.y[mm][t * mg.ldy[mm] + rowr] = tree_final(tr);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ launch
+static int device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Rows per wave: 2 keeps per-wave register use moderate and gives many units to balance;
+// with several tokens per launch the register budget is NT*RPW <= 8 outputs per lane.
+static int pick_rpw(int nt) {
+#ifdef KQ_GEMV_RPW
+    (void)nt;
+    return KQ_GEMV_RPW;
+#else
+    return nt >= 3 ? 1 : 2;
+#endif
+}
+
+template <int TYPE, int NT, int RPW>
+static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s) {
+    MatGroup mg = mg0;
+    int total = 0;
+    for (int i = 0; i < 3; i++) {
+        mg.first_unit[i] = total;
+        if (i < mg.n) total += (int)((mg0.first_unit[i + 1] - mg0.first_unit[i]) * (8 / RPW));
+    }
+    mg.first_unit[3] = total;
+    const int passes = (G + 15) / 16;
+    if (passes <= 4) {
+        // K unit streams of `passes` waves per workgroup (about KQ_GEMV_WG_WAVES waves per
+        // workgroup); about KQ_GEMV_WAVES_PER_CU waves per CU in total
+        const int K = passes >= KQ_GEMV_WG_WAVES ? 1 : KQ_GEMV_WG_WAVES / passes;
+        int streams = device_cus() * KQ_GEMV_WAVES_PER_CU / passes;
+        if (streams > total) streams = total;
+        auto round_xcd = [](int n) { return (n + KQ_XCDS - 1) / KQ_XCDS * KQ_XCDS; };
+        int nwg = round_xcd((streams + K - 1) / K);
+        size_t lds = 0;
+        int kmax = 1;
+        if (passes > 1) {
+            for (;;) {
+                kmax = (total + nwg * K - 1) / (nwg * K);
+                lds = (size_t)K * kmax * NT * RPW * passes * sizeof(float);
+                if (lds <= 32768 || nwg * K >= total) break;
+                nwg = round_xcd(nwg * 2);
+            }
+        }
+        hipLaunchKernelGGL((k_gemv_q8k_split<TYPE, NT, RPW>), dim3(nwg), dim3(64 * passes * K), lds, s, mg, xq, G,
+                           total, passes, kmax);
+        return;
+    }
     const int wpb = 4;
-    dim3 grid((unsigned)((waves + wpb - 1) / wpb)), block(64 * wpb);
-    if (type == TYPE_Q4_K)
-        hipLaunchKernelGGL((k_gemv_q4k_q8k<NT, RPW>), grid, block, 0, s, w, xq, y, R, G, ldy);
+    int waves = device_cus() * KQ_GEMV_WAVES_PER_CU;
+    if (waves > total) waves = total;
+    dim3 grid((waves + wpb - 1) / wpb), block(64 * wpb);
+    if (G <= 16)
+        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, true>), grid, block, 0, s, mg, xq, G, total);
     else
-        hipLaunchKernelGGL((k_gemv_q6k_q8k<NT, RPW>), grid, block, 0, s, w, xq, y, R, G, ldy);
+        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false>), grid, block, 0, s, mg, xq, G, total);
 }
 
-template <int NT>
-static void launch_rpw(const uint8_t* w, int R, int G, int type, const uint8_t* xq, float* y,
-                       int64_t ldy, int rpw, hipStream_t s) {
+template <int TYPE, int NT>
+static void launch2(const MatGroup& mg, const uint8_t* xq, int G, int rpw, hipStream_t s) {
     switch (rpw) {
-        case 1: launch_nt<NT, 1>(w, R, G, type, xq, y, ldy, s); break;
-        case 2: launch_nt<NT, 2>(w, R, G, type, xq, y, ldy, s); break;
-        case 4: launch_nt<NT, 4>(w, R, G, type, xq, y, ldy, s); break;
-        default: launch_nt<NT, 8>(w, R, G, type, xq, y, ldy, s); break;
+        case 1: launch3<TYPE, NT, 1>(mg, xq, G, s); break;
+        case 2: launch3<TYPE, NT, 2>(mg, xq, G, s); break;
+        case 4: launch3<TYPE, NT, 4>(mg, xq, G, s); break;
+        default: launch3<TYPE, NT, 8>(mg, xq, G, s); break;
     }
 }
 
-// Rows per wave: enough waves to cover the chip (>= 2048) for the given row count, and a
-// register budget of NT*RPW <= 16 outputs per lane.
-static int pick_rpw(int R, int nt) {
-    int rpw = 8;
-    while (rpw > 1 && ((int64_t)(R / 8) * (8 / rpw) < 2048 || nt * rpw > 16)) rpw >>= 1;
-    return rpw;
+template <int TYPE>
+static void launch1(const MatGroup& mg, const uint8_t* xq, int G, int nt, int rpw, hipStream_t s) {
+    switch (nt) {
+        case 1: launch2<TYPE, 1>(mg, xq, G, rpw, s); break;
+        case 2: launch2<TYPE, 2>(mg, xq, G, rpw, s); break;
+        case 3: launch2<TYPE, 3>(mg, xq, G, rpw, s); break;
+        default: launch2<TYPE, 4>(mg, xq, G, rpw, s); break;
+    }
+}
+
+// n matrices of one type sharing xq (N tokens); tokens go in groups of up to 4 per launch, each
+// group an independent launch over the same weights.  first_unit[] is filled with row-tile
+// prefix counts here and scaled to units per RPW in launch3.
+void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
+                           const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s) {
+    const int G = C / QK;
+    for (int n0 = 0; n0 < N; n0 += 4) {
+        const int nt = N - n0 < 4 ? N - n0 : 4;
+        MatGroup mg{};
+        mg.n = n;
+        int tiles = 0;
+        for (int i = 0; i < n; i++) {
+            mg.w[i] = w[i];
+            mg.y[i] = y[i] + (int64_t)n0 * ldy[i];
+            mg.ldy[i] = ldy[i];
+            mg.first_unit[i] = tiles;
+            tiles += R[i] / 8;
+        }
+        for (int i = n; i < 4; i++) mg.first_unit[i] = tiles;
+        const uint8_t* xg = xq + (int64_t)n0 * G * Q8K_BYTES;
+        if (type == TYPE_Q4_K) launch1<TYPE_Q4_K>(mg, xg, G, nt, pick_rpw(nt), s);
+        else launch1<TYPE_Q6_K>(mg, xg, G, nt, pick_rpw(nt), s);
+    }
 }
 
 void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N, float* y,
                      int64_t ldy, int rows_per_wave, hipStream_t s) {
-    const int G = C / QK;
-    // Tokens go in groups of up to 4 per launch; each group is an independent launch over the
-    // same weights, so every token's arithmetic is the same as in a single-token call.
-    for (int n0 = 0; n0 < N; n0 += 4) {
-        const int nt = N - n0 < 4 ? N - n0 : 4;
-        const int rpw = rows_per_wave > 0 ? rows_per_wave : pick_rpw(R, nt);
-        const uint8_t* xg = xq + (int64_t)n0 * G * Q8K_BYTES;
-        float* yg = y + (int64_t)n0 * ldy;
-        switch (nt) {
-            case 1: launch_rpw<1>(w, R, G, type, xg, yg, ldy, rpw, s); break;
-            case 2: launch_rpw<2>(w, R, G, type, xg, yg, ldy, rpw, s); break;
-            case 3: launch_rpw<3>(w, R, G, type, xg, yg, ldy, rpw, s); break;
-            default: launch_rpw<4>(w, R, G, type, xg, yg, ldy, rpw, s); break;
-        }
-    }
+    (void)rows_per_wave;
+    launch_gemv_q8k_group(1, &w, &R, C, type, xq, N, &y, &ldy, s);
 }
 
 }  // namespace kq

@@ -41,9 +41,8 @@ __device__ __forceinline__ uint32_t ld4(const uint8_t* p) {          // p 4-byte
 // 16 bytes at a 2-byte aligned address, read as dword-aligned loads and funnel-shifted.
 // Reads the dword-aligned span [p & ~3, (p & ~3) + 20): callers guarantee it lies in the buffer.
 __device__ __forceinline__ u32x4 ld16_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint8_t* q = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-    const uint32_t sh = uint32_t(a & 3);
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint8_t* q = p - sh;     // pointer arithmetic keeps the global address space
     const u32x4 v = ld16_a4(q);
     const uint32_t e = ld4(q + 16);
     u32x4 r;
@@ -77,45 +76,53 @@ __device__ __forceinline__ uint32_t byte_of(uint32_t w, int k) { return (w >> (8
 // are ((s2 >> 4) & 0x0f0f0f0f) | ((s1 >> 2) & 0x30303030).
 struct ScMin { uint32_t sc_lo, sc_hi, m_lo, m_hi; };
 __device__ __forceinline__ ScMin q4k_scmin_pair(uint32_t s0, uint32_t s1, uint32_t s2, int p) {
-    uint32_t scw, mw;
-    if (p < 2) {
-        scw = s0 & 0x3f3f3f3fu;
-        mw = s1 & 0x3f3f3f3fu;
-    } else {
-        scw = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
-        mw = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
-    }
-    const int k0 = (2 * p) & 3;
+    // both candidates are formed and one is selected, so the code has no divergent branch
+    const uint32_t sc_a = s0 & 0x3f3f3f3fu, m_a = s1 & 0x3f3f3f3fu;
+    const uint32_t sc_b = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t m_b = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+    const bool hi = p >= 2;
+    const uint32_t scw = hi ? sc_b : sc_a, mw = hi ? m_b : m_a;
+    const int sh = 16 * (p & 1);   // sub-blocks 2p, 2p+1 are bytes (2p)&3, (2p)&3 + 1
     ScMin r;
-    r.sc_lo = byte_of(scw, k0);
-    r.sc_hi = byte_of(scw, k0 + 1);
-    r.m_lo = byte_of(mw, k0);
-    r.m_hi = byte_of(mw, k0 + 1);
+    r.sc_lo = (scw >> sh) & 0xffu;
+    r.sc_hi = (scw >> (sh + 8)) & 0xffu;
+    r.m_lo = (mw >> sh) & 0xffu;
+    r.m_hi = (mw >> (sh + 8)) & 0xffu;
     return r;
 }
 
 // Wave-level helpers.  The lane order of every fp32 reduction below is part of the numerical
 // contract of the GEMV kernels (batched results must equal single-token ones bit for bit), so
-// all kernels use these and only these.
-__device__ __forceinline__ int xor_sum_i32(int v, int mask) {
-    return v + __shfl_xor(v, mask, 64);
+// all kernels use these and only these.  Each step adds a lane's value to its partner's in a
+// butterfly; fp32 addition is commutative, so both partners hold the same bits afterwards.
+constexpr int DPP_QUAD_XOR1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141; // lane j of each 8 <- lane 7-j
+constexpr int DPP_ROW_MIRROR = 0x140;      // lane j of each 16 <- lane 15-j
+constexpr int SWZ_XOR16 = (0x10 << 10) | 0x1F;  // ds_swizzle bit mode: lane ^ 16
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
 }
-__device__ __forceinline__ float xor_sum_f32(float v, int mask) {
-    const float o = __shfl_xor(v, mask, 64);
-    return __fadd_rn(v, o);
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+
 // Sum over the 4 lanes of a quad (lanes 4j..4j+3), exact for int32.
 __device__ __forceinline__ int quad_sum_i32(int v) {
-    v = xor_sum_i32(v, 1);
-    return xor_sum_i32(v, 2);
+    v += dpp<DPP_QUAD_XOR1>(v);
+    return v + dpp<DPP_QUAD_XOR2>(v);
 }
-// Pairwise tree over the 16 super-block slots held by lane bits 2..5 (slot = lane >> 2):
-// ((s0+s1)+(s2+s3)) + ... in natural slot order.
+// Pairwise tree over the 16 super-block slots held by lane bits 2..5 (slot = lane >> 2), for a
+// value that is uniform within each quad: ((s0+s1)+(s2+s3)) + ... in natural slot order.
+// Within a 16-lane row the mirrors pair quad 0 with 1 and 2 with 3, then the two halves.
 __device__ __forceinline__ float slot_tree_f32(float v) {
-    v = xor_sum_f32(v, 4);
-    v = xor_sum_f32(v, 8);
-    v = xor_sum_f32(v, 16);
-    return xor_sum_f32(v, 32);
+    v = __fadd_rn(v, dppf<DPP_ROW_HALF_MIRROR>(v));
+    v = __fadd_rn(v, dppf<DPP_ROW_MIRROR>(v));
+    v = __fadd_rn(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), SWZ_XOR16)));
+    return __fadd_rn(v, __shfl_xor(v, 32, 64));
 }
 
 }  // namespace kq

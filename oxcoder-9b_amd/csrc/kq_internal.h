@@ -25,6 +25,9 @@ inline int block_bytes(int type) { return type == KQ_TYPE_Q4_K ? 144 : 210; }
 void launch_q8k_quantize(const float* x, int64_t ldx, int C, int N, uint8_t* xq, hipStream_t s);
 void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N, float* y,
                      int64_t ldy, int rows_per_wave, hipStream_t s);
+// n (1..3) matrices of one type sharing xq; one launch per group of up to 4 tokens.
+void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
+                           const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s);
 void launch_subblock_sums(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N,
                           int32_t* sums, hipStream_t s);
 void launch_gemv_f32(const uint8_t* w, int R, int C, int type, const float* x, float* y,

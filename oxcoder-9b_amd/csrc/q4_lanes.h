@@ -82,15 +82,15 @@ struct PassTree {
 };
 __device__ __forceinline__ void tree_init(PassTree& t) { t.n = 0; }
 __device__ __forceinline__ void tree_push(PassTree& t, float v) {
-    int l = 0;
+    bool carry = true;   // v still has to be placed
 #pragma unroll
-    for (; l < TREE_LEVELS; l++) {
-        if (!((t.n >> l) & 1)) break;
-        v = __fadd_rn(t.s[l], v);
+    for (int l = 0; l < TREE_LEVELS; l++) {
+        const bool bit = (t.n >> l) & 1;
+        const float merged = __fadd_rn(t.s[l], v);
+        if (carry && !bit) t.s[l] = v;
+        if (carry && bit) v = merged;
+        carry = carry && bit;
     }
-#pragma unroll
-    for (int k = 0; k < TREE_LEVELS; k++)
-        if (k == l) t.s[k] = v;
     t.n += 1;
 }
 // Final value: merge pending subtrees from the smallest up, each padded with a zero subtree of

@@ -18,25 +18,26 @@ k_q8k_quantize(const float* __restrict__ x, int64_t ldx, int G, int nblocks, uin
     const float* xb = x + (int64_t)n * ldx + (int64_t)g * QK + 4 * lane;
     const f32x4 v = *reinterpret_cast<const f32x4_a4*>(xb);
 
-    // First (lowest index) element of largest |x| within the lane; NaN never compares greater.
-    float amax = 0.0f, vmax = 0.0f;
-    int idx = 1 << 20;
-    {
-        const float e[4] = {v.x, v.y, v.z, v.w};
+    // max |x| over the block: butterfly max (exact, order-free); NaN never wins (v_max returns
+    // the other operand), matching the strict "ax > amax" scan of the reference definition.
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(e[0]), __builtin_fabsf(e[1])),
+                                 __builtin_fmaxf(__builtin_fabsf(e[2]), __builtin_fabsf(e[3])));
+    amax = __builtin_fmaxf(amax, dppf<DPP_QUAD_XOR1>(amax));
+    amax = __builtin_fmaxf(amax, dppf<DPP_QUAD_XOR2>(amax));
+    amax = __builtin_fmaxf(amax, dppf<DPP_ROW_HALF_MIRROR>(amax));
+    amax = __builtin_fmaxf(amax, dppf<DPP_ROW_MIRROR>(amax));
+    amax = __builtin_fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, amax), SWZ_XOR16)));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, 64));
+    // signed value of the first element with |x| == amax: lowest lane holding one, lowest k in it
+    float first = 0.0f;
+    bool has = false;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float ax = __builtin_fabsf(e[k]);
-            if (ax > amax) { amax = ax; vmax = e[k]; idx = 4 * lane + k; }
-        }
-    }
-    // Across lanes: larger |x| wins, ties go to the lower index.
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const float oa = __shfl_xor(amax, m, 64);
-        const float ov = __shfl_xor(vmax, m, 64);
-        const int oi = __shfl_xor(idx, m, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; vmax = ov; idx = oi; }
-    }
+    for (int k = 3; k >= 0; k--)
+        if (__builtin_fabsf(e[k]) == amax) { first = e[k]; has = true; }
+    const uint64_t holders = __ballot(has);
+    const int src = holders ? __builtin_ctzll(holders) : 0;
+    const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, first), src));
 
     uint8_t* ob = xq + (int64_t)blk * Q8K_BYTES;
     uint32_t packed = 0;
@@ -44,7 +45,6 @@ k_q8k_quantize(const float* __restrict__ x, int64_t ldx, int G, int nblocks, uin
     float d = 0.0f;
     if (amax != 0.0f) {
         const float iscale = -127.0f / vmax;
-        const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const float t = __fmul_rn(iscale, e[k]);
@@ -56,10 +56,10 @@ k_q8k_quantize(const float* __restrict__ x, int64_t ldx, int G, int nblocks, uin
         d = 1.0f / iscale;
     }
     // 16-value sums: lanes 4j..4j+3 hold values 16j..16j+15.
-    s4 += __shfl_xor(s4, 1, 64);
-    s4 += __shfl_xor(s4, 2, 64);
-    // Pack two adjacent sums (lanes 8k and 8k+4) into one dword for the store.
-    const int s_next = __shfl_xor(s4, 4, 64);
+    s4 = quad_sum_i32(s4);
+    // Pack two adjacent sums (lanes 8k and 8k+4 hold sums 2k, 2k+1) into one dword for the store:
+    // lane 8k reads lane 8k+7 through the half-row mirror.
+    const int s_next = dpp<DPP_ROW_HALF_MIRROR>(s4);
 
     *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = packed;
     if (lane == 0) *reinterpret_cast<float*>(ob) = d;

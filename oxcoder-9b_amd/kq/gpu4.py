@@ -81,8 +81,9 @@ class Engine:
                 ops.gemv(w, R, C_, ty, x, y)
             return 1
         xq = self._quantize(x.reshape(1, -1)[:, :C], C)
-        for (w, R, C_, ty), y in zip(mats, outs):
-            ops.gemv_q8k(w, R, C_, ty, xq, 1, y)
+        # matrices sharing the input go three at a time into one launch (kcpu4.c:100-118)
+        for i in range(0, len(mats), 3):
+            ops.gemv_q8k_multi(mats[i:i + 3], xq, 1, list(outs[i:i + 3]))
         return 1
 
     def gemv_batch(self, names, X, outs):

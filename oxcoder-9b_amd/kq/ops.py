@@ -72,6 +72,33 @@ def gemv_q8k(w, R, C_, ty, xq, N, y, ldy=None):
     return y
 
 
+def gemv_q8k_multi(mats, xq, N, ys):
+    """Up to 3 matrices [(w, R, C, type)] sharing one Q8_K input, one launch per type
+    (kq_gemv_q8k_multi).  ys[i] is [N][ld_i] or [R_i]."""
+    n = len(mats)
+    if not 1 <= n <= 3 or len(ys) != n:
+        raise ValueError("1..3 matrices with one output each")
+    C_ = mats[0][2]
+    if any(m[2] != C_ for m in mats):
+        raise ValueError("matrices sharing an input must have the same column count")
+    W = (C.c_void_p * n)(*[_weights(w, R, C_, ty).value for (w, R, _, ty) in mats])
+    Rs = (C.c_int * n)(*[m[1] for m in mats])
+    Ts = (C.c_int * n)(*[m[3] for m in mats])
+    lds = []
+    for (w, R, _, ty), y in zip(mats, ys):
+        ld = y.stride(0) if y.dim() == 2 else R
+        if y.numel() < (N - 1) * ld + R:
+            raise ValueError("output too small")
+        lds.append(ld)
+    Y = (C.c_void_p * n)(*[_dev(y, "y", torch.float32).value for y in ys])
+    L = (C.c_int64 * n)(*lds)
+    if xq.numel() < N * (C_ // QK) * Q8K_BYTES:
+        raise ValueError("xq too small")
+    _lib.check(_lib.kq().kq_gemv_q8k_multi(n, W, Rs, C_, Ts, _dev(xq, "xq", torch.uint8), N, Y, L,
+                                           _stream(mats[0][0].device)))
+    return ys
+
+
 def gemm_q8k(w, R, C_, ty, xq, M, y, ldy=None):
     """Y[m][r] for M Q8_K activation rows (kq_gemm_q8k, prefill)."""
     pw = _weights(w, R, C_, ty)

@@ -175,6 +175,25 @@ def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
     assert_close_inf(s, orc.gemv_q8k(host(W), R, C, ty, xq, 16))
 
 
+@pytest.mark.parametrize("N", [1, 3, 6])
+def test_gemv_q8k_multi_matches_single(dev, orc, N):
+    """q/k/v-style group (two Q4_K, one Q6_K) in one call equals three single calls bit for bit."""
+    C = 4096
+    mats_h = [(synth(R, C, ty, 50 + i), R, C, ty) for i, (R, ty) in enumerate([(4096, 12), (1024, 12), (1024, 14)])]
+    mats = [(dev_t(W, dev), R, C_, ty) for (W, R, C_, ty) in mats_h]
+    xq = orc.quantize_q8k(kqq.synthetic_activations(N, C, seed=N))
+    xqd = dev_t(xq, dev)
+    ys = [torch.full((N, R + 4), -7.0, device=dev) for (_, R, _, _) in mats]
+    ops.gemv_q8k_multi(mats, xqd, N, ys)
+    for (w, R, C_, ty), y, (W, _, _, _) in zip(mats, ys, mats_h):
+        ref = torch.empty((N, R), device=dev)
+        ops.gemv_q8k(w, R, C_, ty, xqd, N, ref)
+        got = host(y)
+        np.testing.assert_array_equal(got[:, :R], host(ref))
+        assert np.all(got[:, R:] == -7.0)
+        assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C_, ty, xq, N))
+
+
 @pytest.mark.parametrize("ty,R,C,M", [(12, 512, 4096, 64), (14, 256, 12288, 40)])
 def test_gemm_q8k_vs_oracle(dev, orc, ty, R, C, M):
     W = synth(R, C, ty, 31)

@@ -148,8 +148,9 @@ int kq_gemm_q8k(const void* w, int R, int C, int type, const void* xq, int M, fl
     if (M > 1 && ldy < R) return fail(KQ_ERR_ARG, "%s: ldy=%lld is smaller than R=%d", fn, (long long)ldy, R);
     KQ_TRY(check_ptr(xq, 4, "xq", fn));
     KQ_TRY(check_ptr(y, 4, "y", fn));
-    launch_gemv_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), M, y,
-                    ldy, 0, as_stream(stream));
+    if ((int64_t)M * (C / 256) > 0x7fffffffLL) return fail(KQ_ERR_ARG, "%s: M*C/256 too large", fn);
+    launch_gemm_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), M, y, ldy,
+                    as_stream(stream));
     return check_launch(fn);
 }
 

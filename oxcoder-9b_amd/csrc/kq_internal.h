@@ -28,6 +28,8 @@ void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq
 // n (1..3) matrices of one type sharing xq; one launch per group of up to 4 tokens.
 void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s);
+void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
+                     hipStream_t s);
 void launch_subblock_sums(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N,
                           int32_t* sums, hipStream_t s);
 void launch_gemv_f32(const uint8_t* w, int R, int C, int type, const float* x, float* y,

@@ -194,14 +194,31 @@ def test_gemv_q8k_multi_matches_single(dev, orc, N):
         assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C_, ty, xq, N))
 
 
-@pytest.mark.parametrize("ty,R,C,M", [(12, 512, 4096, 64), (14, 256, 12288, 40)])
+@pytest.mark.parametrize("ty,R,C,M", [
+    (12, 512, 4096, 64), (14, 256, 12288, 40),       # one M tile, partial
+    (12, 136, 256, 300), (14, 136, 256, 300),        # R % 128 = 8, one super-block, ragged M
+    (12, 1024, 4096, 512), (14, 512, 4352, 257),     # several tiles both ways; G = 17
+])
 def test_gemm_q8k_vs_oracle(dev, orc, ty, R, C, M):
     W = synth(R, C, ty, 31)
     X = kqq.synthetic_activations(M, C, seed=M)
     xq = orc.quantize_q8k(X)
-    y = torch.empty((M, R), device=dev)
-    ops.gemm_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), M, y)
-    assert_close_inf(host(y), orc.gemv_q8k(W, R, C, ty, xq, M))
+    y = torch.full((M, R + 8), -3.0, device=dev)
+    ops.gemm_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), M, y, R + 8)
+    got = host(y)
+    assert np.all(got[:, R:] == -3.0)
+    assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C, ty, xq, M))
+
+
+@pytest.mark.parametrize("ty", [12, 14])
+def test_gemm_q8k_reference_inputs(dev, orc, ty):
+    """The reference unit test's random block bytes (any scale/min bit pattern) through the GEMM."""
+    W, x, R, C = reference_unit_inputs()[ty]
+    X = np.stack([x * (i + 1) * (-1) ** i for i in range(37)]).astype(np.float32)
+    xq = orc.quantize_q8k(X)
+    y = torch.empty((37, R), device=dev)
+    ops.gemm_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), 37, y)
+    assert_close_inf(host(y), orc.gemv_q8k(W, R, C, ty, xq, 37))
 
 
 # ------------------------------------------------------------------------------- fp32-x GEMV

@@ -78,9 +78,10 @@ class Runner:
         L = (C.c_int64 * n)(*[m[1] for m in mats])
         self.check(self.lib.kq_gemv_q8k_multi(n, W, Rs, mats[0][2], Ts, C.c_void_p(xq.data_ptr()), 1, Y, L, s))
 
-    def gemm(self, w, R, C_, ty, xq, M, y, s):
-        self.check(self.lib.kq_gemm_q8k(C.c_void_p(w.data_ptr()), R, C_, ty, C.c_void_p(xq.data_ptr()), M,
-                                        C.c_void_p(y.data_ptr()), R, s))
+    def gemm(self, w, R, C_, ty, xq, M, y, ws, s):
+        """kq_gemm_q8k_ws with a preallocated workspace (ws: 256-byte aligned device tensor)."""
+        self.check(self.lib.kq_gemm_q8k_ws(C.c_void_p(w.data_ptr()), R, C_, ty, C.c_void_p(xq.data_ptr()), M,
+                                           C.c_void_p(y.data_ptr()), R, C.c_void_p(ws.data_ptr()), ws.numel(), s))
 
 
 def make_layer(torch, dev, copies):
@@ -228,7 +229,8 @@ def gemm_extra(torch, rn, dev):
             X = torch.from_numpy(kqq.synthetic_activations(M, C_, seed=M)).to(dev)
             xq = ops.q8k_quantize(X)
             y = torch.empty((M, R), device=dev)
-            g = capture(torch, lambda: rn.gemm(w, R, C_, ty, xq, M, y, rn.stream()))
+            ws = torch.empty(ops.gemm_workspace_bytes(C_, M), dtype=torch.uint8, device=dev)
+            g = capture(torch, lambda: rn.gemm(w, R, C_, ty, xq, M, y, ws, rn.stream()))
             time_graphs(torch, [g])
             reps = 3
             el = time_graphs(torch, [g] * reps) / reps

@@ -26,6 +26,9 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-I" + CSRC, "-I" + os.path.join(ROOT, "include"),
 ]
+# Per-source extra flags.  The GEMM keeps its MFMA accumulators in ordinary VGPRs (the epilogue
+# reads them with VALU instructions every super-block; accumulators in AGPRs would need a copy each).
+HIP_EXTRA = {"gemm_q8k.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HOST_SOURCES = ["host/quantize_weights.cpp"]
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
               "-fno-math-errno", "-Wall", "-I" + os.path.join(ROOT, "include")]
@@ -43,7 +46,8 @@ def _run(cmd):
         sys.stderr.write(rest + "\n")
 
 
-def _compile_hip(src, extra=()):
+def _compile_hip(src):
+    extra = HIP_EXTRA.get(src, [])
     obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
     _run([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj

@@ -1,368 +1,409 @@
 // Prefill GEMM for gfx950: Y[m][n] = sum_k x_q8[m][k] * W[n][k], Q4_K / Q6_K weights in the Kindi
 // layout, Q8_K activations, int8 MFMA with int32 accumulation and an fp32 epilogue per super-block.
 //
-// Scale folding.  The 6-bit (Q4_K) or int8 (Q6_K) sub-block scale changes every 32 / 16 columns,
-// faster than an MFMA K step can absorb.  It is folded into the weight: w' = sc*q is 10 bits
-// (Q4_K, 0..945) or 14 bits signed (Q6_K, sc*(q+32) in [-8064, 8001]); written as w' = 128*h + l
-// with l in 0..127 and h small, both are int8, so one super-block (K = 256) is two int8 MFMA
-// sweeps accumulating I1 = sum_k w'*q8 exactly.  The remaining per-sub-block term (Q4_K min:
-// I2 = sum_s m_s*B_s; Q6_K offset: I2 = sum_t sc_t*B_t with B from the Q8_K bsums) is one more
-// small MFMA pair on B split as 64*Bh + Bl.  Per super-block the fp32 epilogue adds
-//   Q4_K: dx * (d * I1 - dmin * I2)        Q6_K: dx * d * (I1 - 32 * I2)
-// (the same per-super-block quantity as the GEMV; the I2 part is added first, then the I1 part,
-// and the fp32 sums run along K in natural order).
+// Weight planes.  The sub-block scale changes every 32 (Q4_K) or 16 (Q6_K) columns, faster than
+// an MFMA K step can absorb, so it is folded into the weights, and the folded weight is split
+// into two int8 planes; one super-block (K = 256) is two int8 MFMA sweeps that accumulate exact
+// integers:
+//   Q4_K  sc (6 bit) = 8a + b with a, b in 0..7; plane H = a*q, plane L = b*q (both <= 105);
+//         I1 = 8 * (x . H) + (x . L) = sum sc*q*x.  Each plane is one packed 16-bit multiply of
+//         four nibbles by a (no carry crosses a byte since a*q < 256).
+//   Q6_K  w = sc*(q-32) in [-4096, 4064] (the -32 offset is folded in as well); v = w + 128 as
+//         int16: plane H = high byte of v (-16..16), plane L = low byte of v ^ 0x80 = low byte of
+//         w as int8; I = 256 * (x . H) + (x . L) = sum w*x.
+// The Q4_K min term I2 = sum_s m_s * B_s (B_s = sum of the activation quants of sub-block s, from
+// the Q8_K bsums) is one fp16 MFMA with K = 16: activation side [B_s >> 6, B_s & 63], weight
+// side [-64 m_s, -m_s]; every operand and product is an exact fp16 / fp32 integer, so the MFMA
+// returns -I2 exactly.  Per super-block the fp32 epilogue adds
+//   Q4_K: dx * (d * I1 - dmin * I2)          Q6_K: dx * (d * I)
+// (the per-super-block quantity of the CPU reference, with fp32 sums along K).
 //
-// Work split.  A workgroup (4 waves) owns a 128 (tokens) x 128 (weight rows) output tile; each
-// wave a 64 x 64 quarter = 2 x 2 MFMA 32x32 tiles.  Per super-block every thread unpacks half a
-// weight row into the two int8 planes in LDS (row stride 272 B, 16-B aligned, staggered banks),
-// while each lane reads its MFMA A operand (16 contiguous activation bytes) straight from the
-// Q8_K block.  The next super-block's weight bytes and activation fragments are loaded into
-// registers while the current one runs.  Rows past M or R are clamped for loading and not stored.
+// Work split.  A workgroup (4 waves) owns 128 tokens x BN weight rows (BN = 128 or 64); each wave
+// a 64 x BN/2 quarter of 32x32 MFMA tiles.  Each thread unpacks BN of the 256 weights of one
+// weight row into the two LDS planes (rows of 256 B, 16-B chunks XOR-swizzled by row so that 16
+// consecutive rows hit distinct banks); the planes are double-buffered, so the next super-block
+// is unpacked while the MFMAs of the current one run, with one barrier per super-block.
+//
+// Activation fragments.  An MFMA A operand holds 16 bytes of each of 32 token rows, so reading
+// it straight from Q8_K rows touches 32-64 cache lines per load instruction, for every weight
+// tile.  A first pass (k_q8k_frag) rewrites the quants once into fragment order,
+//   frag[m/32][g][ks 0..7][lane 0..63][16 B] = qs bytes 32ks + 16(lane/32) .. +15 of row 32(m/32) + lane%32,
+// so each A load is one contiguous 1 KB; rows are padded to a multiple of 128 with zeros.  The
+// next super-block's raw weight bytes and activation fragments are loaded one step ahead.  Rows
+// past R are clamped for loading and not stored.
 #include "kq_device.h"
 #include "kq_internal.h"
-#include "q4_lanes.h"
 
 namespace kq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int GM_BM = 128, GM_BN = 128, GM_WS = 272;   // tile rows, tile cols, LDS row stride
+constexpr int GM_BM = 128;   // tokens per workgroup
 
-// ------------------------------------------------------------------ weight unpack helpers
-// 4 unsigned nibbles (bytes of x, 0..15) times scale s (0..63): w' = s*q split into
-// h = w' >> 7 (0..7) and l = w' & 127, returned as 4 bytes each.  Products are formed two at a
-// time in 16-bit halves (each < 1024, so no carry crosses a half).
-__device__ __forceinline__ void split_q4(uint32_t x, uint32_t s, uint32_t& hb, uint32_t& lb) {
-    const uint32_t e = x & 0x00ff00ffu, o = (x >> 8) & 0x00ff00ffu;
-    const uint32_t pe = __umul24(e, s), po = __umul24(o, s);
-    lb = (pe & 0x007f007fu) | ((po & 0x007f007fu) << 8);
-    hb = ((pe >> 7) & 0x00070007u) | (((po >> 7) & 0x00070007u) << 8);
+// Byte offset of 16-byte chunk `c` (0..15) of LDS plane row `r`: rows are 256 B, the chunk index
+// is XORed with the row's low 4 bits.
+__device__ __forceinline__ int swz(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
+
+// Four bytes q (each < 16) times s in 0..7, per byte: two 16-bit lanes multiplied at once.
+__device__ __forceinline__ uint32_t mul_u8x4(uint32_t q, uint32_t s2) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, s2));
 }
-// 4 unsigned 6-bit codes (bytes of q) times signed scale sc: w' = sc*q in [-8064, 8001] split into
-// h = w' >> 7 (arithmetic, -63..62) and l = w' & 127.  16-bit lanes hold the exact signed product.
-__device__ __forceinline__ void split_q6(uint32_t q, s16x2 s2, uint32_t& hb, uint32_t& lb) {
-    const uint32_t e = q & 0x00ff00ffu, o = (q >> 8) & 0x00ff00ffu;
-    const s16x2 pe = __builtin_bit_cast(s16x2, e) * s2, po = __builtin_bit_cast(s16x2, o) * s2;
-    const uint32_t ue = __builtin_bit_cast(uint32_t, pe), uo = __builtin_bit_cast(uint32_t, po);
-    lb = (ue & 0x007f007fu) | ((uo & 0x007f007fu) << 8);
-    const uint32_t he = __builtin_bit_cast(uint32_t, (s16x2)(pe >> (short)7));
-    const uint32_t ho = __builtin_bit_cast(uint32_t, (s16x2)(po >> (short)7));
-    hb = (he & 0x00ff00ffu) | ((ho & 0x00ff00ffu) << 8);
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {   // exact small integers only
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
-
 __device__ __forceinline__ void st16(int8_t* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     *reinterpret_cast<u32x4*>(p) = u32x4{a, b, c, d};
 }
 
-// Raw bytes of one half weight row (the thread's share of a super-block).
-template <int TYPE> struct RawW;
-template <> struct RawW<TYPE_Q4_K> { u32x4 hdr, q[4]; };
-template <> struct RawW<TYPE_Q6_K> { u32x4 ql[4], qh[2]; uint32_t qle, qhe, sce, dw, sh; u32x2 sc; };
+template <int BN> struct GemmLds {
+    int8_t wh[2][BN * 256];
+    int8_t wl[2][BN * 256];
+    uint32_t wmin[2][BN * 8];      // Q4_K: row n = 16 f16 [-64 m_0..7, -m_0..7]
+    uint32_t xmin[2][GM_BM * 8];   // Q4_K: row m = 16 f16 [B_0..7 >> 6, B_0..7 & 63]
+    float d[2][BN], dm[2][BN], dx[2][GM_BM];
+};
 
-// bk: this row's block; ph: which half of the super-block (columns 128*ph .. 128*ph+127).
-__device__ __forceinline__ void load_raw(RawW<TYPE_Q4_K>& r, const uint8_t* bk, int ph) {
+// ------------------------------------------------------------------ weight parts
+// Each thread owns one part of one weight row per super-block: part pi of PPR (2 or 4) parts.
+//   Q4_K: NPP = 4/PPR consecutive 64-element chunks p (qs bytes 32p..32p+31: sub-blocks 2p, 2p+1).
+//   Q6_K: half h of the super-block and NJ = 4/PPR of its two 16-column slices jj (elements
+//         128h + 32k + 16jj + 0..15 for k = 0..3: ql bytes 64h + 32(k&1) + 16jj, qh bytes
+//         32h + 16jj, scale 8h + 2k + jj).
+template <int TYPE, int PPR> struct RawW;
+template <int PPR> struct RawW<TYPE_Q4_K, PPR> {
+    static constexpr int NPP = 4 / PPR;
+    u32x4 hdr, q[2 * NPP];
+};
+struct Chunk20 { u32x4 v; uint32_t e; };   // 20 bytes from a dword-aligned address
+template <int PPR> struct RawW<TYPE_Q6_K, PPR> {
+    static constexpr int NJ = 4 / PPR;
+    Chunk20 ql[NJ][2], qh[NJ];
+    u32x2 sc;
+    uint32_t sce, dw, sh;
+};
+
+template <int PPR>
+__device__ __forceinline__ void load_raw(RawW<TYPE_Q4_K, PPR>& r, const uint8_t* bk, int pi) {
+    constexpr int NPP = RawW<TYPE_Q4_K, PPR>::NPP;
     r.hdr = ld16(bk);
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.q[i] = ld16(bk + 16 + 64 * ph + 16 * i);   // qs bytes 64ph .. 64ph+63
+    for (int pp = 0; pp < NPP; pp++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) r.q[2 * pp + c] = ld16(bk + 16 + 32 * (pi * NPP + pp) + 16 * c);
 }
-// Q6_K: the block starts at 0 or 2 (mod 4); words are read from the dword at or below each field
-// (all fields share the shift).  The last word read ends at most 2 bytes past the block, inside
-// the next row's block of the same tile column (only for blocks starting at 0 mod 4, which are
-// never the last row of a tile).
-__device__ __forceinline__ void load_raw(RawW<TYPE_Q6_K>& r, const uint8_t* bk, int ph) {
+
+__device__ __forceinline__ Chunk20 ld20(const uint8_t* p) { return Chunk20{ld16_a4(p), ld4(p + 16)}; }
+
+// Q6_K blocks start at 0 or 2 (mod 4); every field is read from the dword at or below it and
+// funnel-shifted by the block's shift.  The last dword read (bytes 208..211 from the aligned
+// base) passes the block end by 2 bytes only for blocks starting at 0 (mod 4), which are never
+// row 7 of a tile column, so the bytes belong to the next block of the same buffer.
+template <int PPR>
+__device__ __forceinline__ void load_raw(RawW<TYPE_Q6_K, PPR>& r, const uint8_t* bk, int pi) {
+    constexpr int NJ = RawW<TYPE_Q6_K, PPR>::NJ;
+    const int h = NJ == 2 ? pi : pi >> 1, jj0 = NJ == 2 ? 0 : pi & 1;
     r.sh = uint32_t(reinterpret_cast<uintptr_t>(bk) & 3);
     const uint8_t* b4 = bk - r.sh;
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.ql[i] = ld16_a4(b4 + 64 * ph + 16 * i);     // ql bytes 64h .. 64h+63
-    r.qle = ld4(b4 + 64 * ph + 64);
-    r.qh[0] = ld16_a4(b4 + 128 + 32 * ph);                                    // qh bytes 32h .. 32h+31
-    r.qh[1] = ld16_a4(b4 + 144 + 32 * ph);
-    r.qhe = ld4(b4 + 160 + 32 * ph);
-    r.sc = *reinterpret_cast<const u32x2_a4*>(b4 + 192 + 8 * ph);            // scales 8h .. 8h+7
-    r.sce = ld4(b4 + 200 + 8 * ph);
+    for (int j = 0; j < NJ; j++) {
+        const int jj = jj0 + j;
+        r.ql[j][0] = ld20(b4 + 64 * h + 16 * jj);
+        r.ql[j][1] = ld20(b4 + 64 * h + 32 + 16 * jj);
+        r.qh[j] = ld20(b4 + 128 + 32 * h + 16 * jj);
+    }
+    r.sc = *reinterpret_cast<const u32x2_a4*>(b4 + 192 + 8 * h);
+    r.sce = ld4(b4 + 200 + 8 * h);
     r.dw = ld4(b4 + 208);
 }
 
-// Unpack into the LDS planes: row pointers wh/wl (K index 0..255), aux row (16 bytes), d/dmin.
-__device__ __forceinline__ void unpack(const RawW<TYPE_Q4_K>& r, int ph, int8_t* wh, int8_t* wl, uint8_t* aux,
-                                       float* d, float* dm) {
+// Unpack into LDS buffer `L.*[buf]`, weight row `row` (0..BN-1).
+template <int PPR, int BN>
+__device__ __forceinline__ void unpack(const RawW<TYPE_Q4_K, PPR>& r, int pi, int row, GemmLds<BN>& L, int buf) {
+    constexpr int NPP = RawW<TYPE_Q4_K, PPR>::NPP;
+    int8_t* wh = L.wh[buf];
+    int8_t* wl = L.wl[buf];
 #pragma unroll
-    for (int pp = 0; pp < 2; pp++) {
-        const int p = 2 * ph + pp;                                  // qs bytes 32p..32p+31: sub-blocks 2p, 2p+1
+    for (int pp = 0; pp < NPP; pp++) {
+        const int p = pi * NPP + pp;
         const ScMin sm = q4k_scmin_pair(r.hdr.y, r.hdr.z, r.hdr.w, p);
+        const uint32_t alo = (sm.sc_lo >> 3) * 0x10001u, blo = (sm.sc_lo & 7u) * 0x10001u;
+        const uint32_t ahi = (sm.sc_hi >> 3) * 0x10001u, bhi = (sm.sc_hi & 7u) * 0x10001u;
 #pragma unroll
-        for (int c = 0; c < 2; c++) {                               // 16-byte chunk c: elements j = 16c .. 16c+15
+        for (int c = 0; c < 2; c++) {          // elements 64p + 16c + 0..15 (lo), 64p + 32 + 16c (hi)
             const u32x4 v = r.q[2 * pp + c];
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-            uint32_t lh[4], ll[4], hh[4], hl[4];
+            uint32_t h0[4], l0[4], h1[4], l1[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                split_q4(w[i] & 0x0f0f0f0fu, sm.sc_lo, lh[i], ll[i]);         // sub-block 2p
-                split_q4((w[i] >> 4) & 0x0f0f0f0fu, sm.sc_hi, hh[i], hl[i]);  // sub-block 2p+1
+                const uint32_t lo = w[i] & 0x0f0f0f0fu, hi = (w[i] >> 4) & 0x0f0f0f0fu;
+                h0[i] = mul_u8x4(lo, alo);
+                l0[i] = mul_u8x4(lo, blo);
+                h1[i] = mul_u8x4(hi, ahi);
+                l1[i] = mul_u8x4(hi, bhi);
             }
-            const int k_lo = 64 * p + 16 * c, k_hi = 64 * p + 32 + 16 * c;
-            st16(wh + k_lo, lh[0], lh[1], lh[2], lh[3]);
-            st16(wl + k_lo, ll[0], ll[1], ll[2], ll[3]);
-            st16(wh + k_hi, hh[0], hh[1], hh[2], hh[3]);
-            st16(wl + k_hi, hl[0], hl[1], hl[2], hl[3]);
+            const int c0 = 4 * p + c, c1 = 4 * p + 2 + c;   // 16-byte chunk indices
+            st16(wh + swz(row, c0), h0[0], h0[1], h0[2], h0[3]);
+            st16(wl + swz(row, c0), l0[0], l0[1], l0[2], l0[3]);
+            st16(wh + swz(row, c1), h1[0], h1[1], h1[2], h1[3]);
+            st16(wl + swz(row, c1), l1[0], l1[1], l1[2], l1[3]);
         }
-        aux[2 * p] = (uint8_t)sm.m_lo;
-        aux[2 * p + 1] = (uint8_t)sm.m_hi;
+        const float mlo = (float)sm.m_lo, mhi = (float)sm.m_hi;
+        L.wmin[buf][row * 8 + p] = pk_f16(-64.0f * mlo, -64.0f * mhi);
+        L.wmin[buf][row * 8 + 4 + p] = pk_f16(-mlo, -mhi);
     }
-    if (ph == 0) {
-        *d = f16_lo(r.hdr.x);
-        *dm = f16_hi(r.hdr.x);
-    }
+    // every part of the row stores the same d / dmin: no branch in the main loop
+    L.d[buf][row] = f16_lo(r.hdr.x);
+    L.dm[buf][row] = f16_hi(r.hdr.x);
 }
 
-__device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K>& r, int ph, int8_t* wh, int8_t* wl, uint8_t* aux,
-                                       float* d, float* dm) {
-    (void)dm;
-    uint32_t ql[16], qh[8];
-    {
-        const uint32_t a[17] = {r.ql[0].x, r.ql[0].y, r.ql[0].z, r.ql[0].w, r.ql[1].x, r.ql[1].y, r.ql[1].z,
-                                r.ql[1].w, r.ql[2].x, r.ql[2].y, r.ql[2].z, r.ql[2].w, r.ql[3].x, r.ql[3].y,
-                                r.ql[3].z, r.ql[3].w, r.qle};
+template <int PPR, int BN>
+__device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, int row, GemmLds<BN>& L, int buf) {
+    constexpr int NJ = RawW<TYPE_Q6_K, PPR>::NJ;
+    const int h = NJ == 2 ? pi : pi >> 1, jj0 = NJ == 2 ? 0 : pi & 1;
+    int8_t* wh = L.wh[buf];
+    int8_t* wl = L.wl[buf];
+    const uint32_t sh = r.sh;
+    const uint32_t s0 = __builtin_amdgcn_alignbyte(r.sc.y, r.sc.x, sh);   // scales 8h .. 8h+3
+    const uint32_t s1 = __builtin_amdgcn_alignbyte(r.sce, r.sc.y, sh);    // scales 8h+4 .. 8h+7
 #pragma unroll
-        for (int i = 0; i < 16; i++) ql[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], r.sh);
-        const uint32_t b[9] = {r.qh[0].x, r.qh[0].y, r.qh[0].z, r.qh[0].w, r.qh[1].x, r.qh[1].y, r.qh[1].z,
-                               r.qh[1].w, r.qhe};
+    for (int j = 0; j < NJ; j++) {
+        const int jj = jj0 + j;
+        uint32_t Lw[2][4], Hw[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) qh[i] = __builtin_amdgcn_alignbyte(b[i + 1], b[i], r.sh);
-    }
-    const uint32_t sc0 = __builtin_amdgcn_alignbyte(r.sc.y, r.sc.x, r.sh);   // scales 8h .. 8h+3
-    const uint32_t sc1 = __builtin_amdgcn_alignbyte(r.sce, r.sc.y, r.sh);    // scales 8h+4 .. 8h+7
+        for (int t = 0; t < 2; t++) {
+            const Chunk20 c = r.ql[j][t];
+            Lw[t][0] = __builtin_amdgcn_alignbyte(c.v.y, c.v.x, sh);
+            Lw[t][1] = __builtin_amdgcn_alignbyte(c.v.z, c.v.y, sh);
+            Lw[t][2] = __builtin_amdgcn_alignbyte(c.v.w, c.v.z, sh);
+            Lw[t][3] = __builtin_amdgcn_alignbyte(c.e, c.v.w, sh);
+        }
+        {
+            const Chunk20 c = r.qh[j];
+            Hw[0] = __builtin_amdgcn_alignbyte(c.v.y, c.v.x, sh);
+            Hw[1] = __builtin_amdgcn_alignbyte(c.v.z, c.v.y, sh);
+            Hw[2] = __builtin_amdgcn_alignbyte(c.v.w, c.v.z, sh);
+            Hw[3] = __builtin_amdgcn_alignbyte(c.e, c.v.w, sh);
+        }
 #pragma unroll
-    for (int k = 0; k < 4; k++) {                     // element e = 128h + 32k + j
-#pragma unroll
-        for (int c = 0; c < 2; c++) {                 // j = 16c .. 16c+15: sub-block 8h + 2k + c
-            const uint32_t scw = k < 2 ? sc0 : sc1;
-            const int scv = (int)(int8_t)(uint8_t)(scw >> (8 * ((2 * k + c) & 3)));
-            const s16x2 s2 = {(short)scv, (short)scv};
+        for (int k = 0; k < 4; k++) {              // elements 128h + 32k + 16jj + 0..15
+            const uint32_t scw = k < 2 ? s0 : s1;
+            const int sc = (int)(int8_t)(uint8_t)(scw >> (8 * ((2 * k + jj) & 3)));
+            const uint32_t s2 = (uint32_t)(sc & 0xffff) * 0x10001u;
+            const uint32_t c2 = (uint32_t)((128 - 32 * sc) & 0xffff) * 0x10001u;
             uint32_t hb[4], lb[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t L = ql[8 * (k & 1) + 4 * c + i], H = qh[4 * c + i];
-                const uint32_t q = ((L >> (4 * (k >> 1))) & 0x0f0f0f0fu) | (((H >> (2 * k)) & 0x03030303u) << 4);
-                split_q6(q, s2, hb[i], lb[i]);
+                const uint32_t lq = (Lw[k & 1][i] >> (4 * (k >> 1))) & 0x0f0f0f0fu;
+                const uint32_t hq = ((Hw[i] >> (2 * k)) & 0x03030303u) << 4;
+                const uint32_t q = lq | hq;                                  // 6-bit codes, 4 bytes
+                const uint32_t e = __builtin_amdgcn_perm(0u, q, 0x0c020c00u);    // bytes 0, 2 -> 16-bit lanes
+                const uint32_t o = __builtin_amdgcn_perm(0u, q, 0x0c030c01u);    // bytes 1, 3
+                const s16x2 sv = __builtin_bit_cast(s16x2, s2), cv = __builtin_bit_cast(s16x2, c2);
+                const uint32_t ve = __builtin_bit_cast(uint32_t, (s16x2)(__builtin_bit_cast(s16x2, e) * sv + cv));
+                const uint32_t vo = __builtin_bit_cast(uint32_t, (s16x2)(__builtin_bit_cast(s16x2, o) * sv + cv));
+                hb[i] = __builtin_amdgcn_perm(vo, ve, 0x07030501u);              // high bytes, element order
+                lb[i] = __builtin_amdgcn_perm(vo, ve, 0x06020400u) ^ 0x80808080u;
             }
-            const int kk = 128 * ph + 32 * k + 16 * c;
-            st16(wh + kk, hb[0], hb[1], hb[2], hb[3]);
-            st16(wl + kk, lb[0], lb[1], lb[2], lb[3]);
+            const int ch = 8 * h + 2 * k + jj;
+            st16(wh + swz(row, ch), hb[0], hb[1], hb[2], hb[3]);
+            st16(wl + swz(row, ch), lb[0], lb[1], lb[2], lb[3]);
         }
     }
-    *reinterpret_cast<uint32_t*>(aux + 8 * ph) = sc0;
-    *reinterpret_cast<uint32_t*>(aux + 8 * ph + 4) = sc1;
-    if (ph == 0) *d = f16_lo(r.dw >> (8 * r.sh));
+    L.d[buf][row] = f16_lo(r.dw >> (8 * sh));   // same value from every part of the row
 }
 
-// ------------------------------------------------------------------ activation-side operands
-// bsums of one Q8_K block (16 int16 in 8 dwords) -> the min-term A operand for this lane's half:
-// Q4_K: B_s = b_2s + b_2s+1 (s < 8), half 0 gets B_s & 63, half 1 gets B_s >> 6, 8 bytes (K = 16).
-// Q6_K: B_t = b_t (t < 16), same split, 16 bytes (K = 32).
-__device__ __forceinline__ uint32_t pack_split(int B0, int B1, int B2, int B3, int half) {
-    const int v0 = half ? (B0 >> 6) : (B0 & 63), v1 = half ? (B1 >> 6) : (B1 & 63);
-    const int v2 = half ? (B2 >> 6) : (B2 & 63), v3 = half ? (B3 >> 6) : (B3 & 63);
-    return (uint32_t)(v0 & 255) | ((uint32_t)(v1 & 255) << 8) | ((uint32_t)(v2 & 255) << 16) | ((uint32_t)v3 << 24);
+// ------------------------------------------------------------------ activation side
+// XP (2 or 4) threads share an activation row: thread part xp holds bsums (16/XP) xp .. +16/XP-1,
+// i.e. NB = 8/XP of the Q4_K sub-block sums, and the row's d.
+template <int XP> struct RawX {
+    static constexpr int NB = 8 / XP;
+    uint32_t bs[NB], d;
+};
+
+template <int XP>
+__device__ __forceinline__ void load_x(RawX<XP>& r, const uint8_t* xb, int xp) {
+    const uint8_t* p = xb + 260 + 4 * RawX<XP>::NB * xp;
+    if constexpr (RawX<XP>::NB == 4) {
+        const u32x4 v = ld16_a4(p);
+        r.bs[0] = v.x; r.bs[1] = v.y; r.bs[2] = v.z; r.bs[3] = v.w;
+    } else {
+        const u32x2 v = *reinterpret_cast<const u32x2_a4*>(p);
+        r.bs[0] = v.x; r.bs[1] = v.y;
+    }
+    r.d = ld4(xb);
+}
+
+template <int TYPE, int XP, int BN>
+__device__ __forceinline__ void stage_x(const RawX<XP>& r, int mr, int xp, GemmLds<BN>& L, int buf) {
+    constexpr int NB = RawX<XP>::NB;
+    if (TYPE == TYPE_Q4_K) {
+        // B_s = bsum[2s] + bsum[2s+1] for s = NB*xp .. NB*xp+NB-1, split as 64 * (B >> 6) + (B & 63)
+        int B[NB];
+#pragma unroll
+        for (int i = 0; i < NB; i++) B[i] = (int)(int16_t)(r.bs[i] & 0xffffu) + (int)(int16_t)(r.bs[i] >> 16);
+#pragma unroll
+        for (int i = 0; i < NB; i += 2) {
+            const int dw = mr * 8 + (NB * xp + i) / 2;
+            L.xmin[buf][dw] = pk_f16((float)(B[i] >> 6), (float)(B[i + 1] >> 6));
+            L.xmin[buf][dw + 4] = pk_f16((float)(B[i] & 63), (float)(B[i + 1] & 63));
+        }
+    }
+    L.dx[buf][mr] = __builtin_bit_cast(float, r.d);   // same value from every part of the row
 }
 
 // ------------------------------------------------------------------ the kernel
-template <int TYPE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restrict__ XQ, int M,
-           float* __restrict__ Y, int64_t ldy) {
+// WN waves along n (2 or 4) times 2 along m; each wave owns 64 tokens x BN/WN weight rows.
+template <int TYPE, int BN, int WN>
+__global__ void __launch_bounds__(128 * WN)
+k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restrict__ XQ,
+           const uint8_t* __restrict__ XF, int M, float* __restrict__ Y, int64_t ldy) {
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
-    __shared__ __attribute__((aligned(16))) int8_t sWh[GM_BN * GM_WS];
-    __shared__ __attribute__((aligned(16))) int8_t sWl[GM_BN * GM_WS];
-    __shared__ __attribute__((aligned(16))) uint8_t sAux[GM_BN * 16];
-    __shared__ float sD[GM_BN], sDm[GM_BN], sDx[GM_BM];
+    constexpr int NTHR = 128 * WN;
+    constexpr int NE = BN / WN;                   // weight rows per wave
+    constexpr int NT = NE / 32;                   // 32-column MFMA tiles per wave
+    constexpr int PPR = NTHR / BN;                // unpack parts per weight row
+    constexpr int XP = NTHR / GM_BM;              // staging parts per activation row
+    constexpr int SHIFT = TYPE == TYPE_Q4_K ? 3 : 8;
+    static_assert(PPR == 2 || PPR == 4, "a weight row is split in 2 or 4 parts");
+    static_assert(NT >= 1, "at least one 32-row tile per wave");
+    __shared__ __attribute__((aligned(16))) GemmLds<BN> L;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave & 1, wn = wave >> 1;
     const int half = lane >> 5, l32 = lane & 31;
-    const int n0 = blockIdx.x * GM_BN, m0 = blockIdx.y * GM_BM;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * GM_BM;
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
 
-    // activation rows this lane feeds (clamped), and the dx row this thread stages
-    const uint8_t* arow[2];
+    // A operand fragments of this lane: tile (m0 + 64 wm + 32 mt) / 32, 8 KB per super-block
+    const uint8_t* afrag[2];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-        int m = m0 + 64 * wm + 32 * mt + l32;
-        m = m < M ? m : M - 1;
-        arow[mt] = XQ + m * xrow;
-    }
-    const uint8_t* dxrow = XQ + (int64_t)(m0 + (tid & 127) < M ? m0 + (tid & 127) : M - 1) * xrow;
+    for (int mt = 0; mt < 2; mt++)
+        afrag[mt] = XF + ((int64_t)(blockIdx.y * 4 + 2 * wm + mt) * G * 512 + lane) * 16;
+    // activation row staged by this thread
+    const int mr = tid & 127, xp = tid >> 7;
+    const uint8_t* xstage = XQ + (int64_t)(m0 + mr < M ? m0 + mr : M - 1) * xrow;
+    // weight row part unpacked by this thread
+    const int prow = tid % BN, pi = tid / BN;
+    const int pr = n0 + prow < R ? n0 + prow : R - 1;
+    const uint8_t* wrow = W + ((int64_t)(pr >> 3) * G * 8 + (pr & 7)) * BS;   // block (pr, g) = wrow + g*8*BS
 
-    // weight half-row this thread unpacks
-    const int pn = tid >> 1, ph = tid & 1;
-    const int pr = n0 + pn < R ? n0 + pn : R - 1;
-    const uint8_t* prow = W + ((int64_t)(pr >> 3) * G * 8 + (pr & 7)) * BS;   // block (pr, g) = prow + g*8*BS
-
-    float yacc[2][2][16];
+    float yacc[2][NT][16];
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++)
+        for (int nt = 0; nt < NT; nt++)
 #pragma unroll
             for (int a = 0; a < 16; a++) yacc[mt][nt][a] = 0.0f;
 
-    RawW<TYPE> raw;
-    u32x4 afr[2][8], bsr[2][2];
-    float dxv = 0.0f;
-    load_raw(raw, prow, ph);
+    // ---- prologue: super-block 0 staged, super-block 1's raw bytes in registers
+    RawW<TYPE, PPR> raw;
+    RawX<XP> rx;
+    v4i afr[2][8];
+    load_raw(raw, wrow, pi);
+    load_x(rx, xstage, xp);
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
+    for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) afr[mt][ks] = ld16_a4(arow[mt] + 4 + 32 * ks + 16 * half);
-        bsr[mt][0] = ld16_a4(arow[mt] + 260);
-        bsr[mt][1] = ld16_a4(arow[mt] + 276);
+        for (int ks = 0; ks < 8; ks++) afr[mt][ks] = __builtin_bit_cast(v4i, ld16(afrag[mt] + ks * 1024));
+    unpack(raw, pi, prow, L, 0);
+    stage_x<TYPE>(rx, mr, xp, L, 0);
+    {
+        const int g1 = G > 1 ? 1 : 0;
+        load_raw(raw, wrow + (int64_t)g1 * 8 * BS, pi);
+        load_x(rx, xstage + (int64_t)g1 * Q8K_BYTES, xp);
     }
-    dxv = __builtin_bit_cast(float, ld4(dxrow));
+    __syncthreads();
 
+    const int nrow0 = wn * NE + l32;        // this lane's B rows: nrow0 + 32 nt
     for (int g = 0; g < G; g++) {
-        // ---- unpack this super-block's weights into LDS
-        unpack(raw, ph, sWh + pn * GM_WS, sWl + pn * GM_WS, sAux + pn * 16, sD + pn, sDm + pn);
-        if (tid < GM_BM) sDx[tid] = dxv;
-        __syncthreads();
+        const int cur = g & 1, nxt = cur ^ 1;
 
-        // ---- operands of this super-block, then prefetch the next one's
-        u32x4 acur[2][8], bcur[2][2];
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) acur[mt][ks] = afr[mt][ks];
-            bcur[mt][0] = bsr[mt][0];
-            bcur[mt][1] = bsr[mt][1];
-        }
-        if (g + 1 < G) {
-            load_raw(raw, prow + (int64_t)(g + 1) * 8 * BS, ph);
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const uint8_t* xb = arow[mt] + (int64_t)(g + 1) * Q8K_BYTES;
-#pragma unroll
-                for (int ks = 0; ks < 8; ks++) afr[mt][ks] = ld16_a4(xb + 4 + 32 * ks + 16 * half);
-                bsr[mt][0] = ld16_a4(xb + 260);
-                bsr[mt][1] = ld16_a4(xb + 276);
-            }
-            dxv = __builtin_bit_cast(float, ld4(dxrow + (int64_t)(g + 1) * Q8K_BYTES));
-        }
-
-        // ---- min / offset term: I2 = 64 * (A_h . B) + A_l . B, applied to the fp32 sums at once
-        //      Q4_K: y -= dx * dmin * I2          Q6_K: y -= dx * d * 32 * I2
+        // ---- stage super-block g+1 into the other buffer (last iteration: a harmless repeat),
+        //      then fetch the raw bytes of g+2
+        unpack(raw, pi, prow, L, nxt);
+        stage_x<TYPE>(rx, mr, xp, L, nxt);
         {
-            const int ncol[2] = {64 * wn + l32, 64 * wn + 32 + l32};
-            if (TYPE == TYPE_Q4_K) {
-                long am[2];
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++) {
-                    const uint32_t w[8] = {bcur[mt][0].x, bcur[mt][0].y, bcur[mt][0].z, bcur[mt][0].w,
-                                           bcur[mt][1].x, bcur[mt][1].y, bcur[mt][1].z, bcur[mt][1].w};
-                    int B[8];
-#pragma unroll
-                    for (int s = 0; s < 8; s++) B[s] = shalf(w[s], 0) + shalf(w[s], 1);
-                    const uint32_t lo = pack_split(B[0], B[1], B[2], B[3], half);
-                    const uint32_t hi = pack_split(B[4], B[5], B[6], B[7], half);
-                    am[mt] = (long)(((uint64_t)hi << 32) | lo);
-                }
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    const long mn = *reinterpret_cast<const long*>(sAux + ncol[nt] * 16);
-                    const long b_lo = half ? 0L : mn, b_hi = half ? mn : 0L;
-                    const float dm = sDm[ncol[nt]];
-#pragma unroll
-                    for (int mt = 0; mt < 2; mt++) {
-                        v16i c = {};
-                        c = __builtin_amdgcn_mfma_i32_32x32x16_i8(am[mt], b_hi, c, 0, 0, 0);
-#pragma unroll
-                        for (int a = 0; a < 16; a++) c[a] <<= 6;
-                        c = __builtin_amdgcn_mfma_i32_32x32x16_i8(am[mt], b_lo, c, 0, 0, 0);
-#pragma unroll
-                        for (int a = 0; a < 16; a++) {
-                            const float dx = sDx[64 * wm + 32 * mt + (a >> 2) * 8 + half * 4 + (a & 3)];
-                            yacc[mt][nt][a] = __builtin_fmaf(dx, -__fmul_rn(dm, (float)c[a]), yacc[mt][nt][a]);
-                        }
-                    }
-                }
-            } else {
-                v4i am[2];
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++) {
-                    const uint32_t w[8] = {bcur[mt][0].x, bcur[mt][0].y, bcur[mt][0].z, bcur[mt][0].w,
-                                           bcur[mt][1].x, bcur[mt][1].y, bcur[mt][1].z, bcur[mt][1].w};
-                    uint32_t pk[4];
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        pk[i] = pack_split(shalf(w[2 * i], 0), shalf(w[2 * i], 1), shalf(w[2 * i + 1], 0),
-                                           shalf(w[2 * i + 1], 1), half);
-                    am[mt] = v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
-                }
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    const u32x4 scv = *reinterpret_cast<const u32x4*>(sAux + ncol[nt] * 16);
-                    const v4i sc = __builtin_bit_cast(v4i, scv), zero = {0, 0, 0, 0};
-                    const v4i b_lo = half ? zero : sc, b_hi = half ? sc : zero;
-                    const float d = sD[ncol[nt]];
-#pragma unroll
-                    for (int mt = 0; mt < 2; mt++) {
-                        v16i c = {};
-                        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(am[mt], b_hi, c, 0, 0, 0);
-#pragma unroll
-                        for (int a = 0; a < 16; a++) c[a] <<= 6;
-                        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(am[mt], b_lo, c, 0, 0, 0);
-#pragma unroll
-                        for (int a = 0; a < 16; a++) {
-                            const float dx = sDx[64 * wm + 32 * mt + (a >> 2) * 8 + half * 4 + (a & 3)];
-                            yacc[mt][nt][a] = __builtin_fmaf(dx, -__fmul_rn(d, (float)(32 * c[a])), yacc[mt][nt][a]);
-                        }
-                    }
-                }
-            }
+            const int g2 = g + 2 < G ? g + 2 : G - 1;
+            load_raw(raw, wrow + (int64_t)g2 * 8 * BS, pi);
+            load_x(rx, xstage + (int64_t)g2 * Q8K_BYTES, xp);
         }
 
-        // ---- main sweeps: I1 = 128 * (A . Wh) + A . Wl over K = 256
-        v16i acch[2][2], accl[2][2];
+        // ---- main sweeps: I = 2^SHIFT * (A . H) + (A . L)
+        v16i acc[2][NT];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            v4i b[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int r = nrow0 + 32 * nt;
+                b[nt] = *reinterpret_cast<const v4i*>(L.wh[cur] + swz(r, 2 * ks + half));
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt],
+                                                                        ks == 0 ? v16i{} : acc[mt][nt], 0, 0, 0);
+        }
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                acch[mt][nt] = v16i{};
-                accl[mt][nt] = v16i{};
-            }
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int a = 0; a < 16; a++) acc[mt][nt][a] <<= SHIFT;
+        const int gn = g + 1 < G ? g + 1 : G - 1;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
-            v4i bh[2], bl[2];
+            v4i b[NT];
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                const int off = (64 * wn + 32 * nt + l32) * GM_WS + 32 * ks + 16 * half;
-                bh[nt] = *reinterpret_cast<const v4i*>(sWh + off);
-                bl[nt] = *reinterpret_cast<const v4i*>(sWl + off);
+            for (int nt = 0; nt < NT; nt++) {
+                const int r = nrow0 + 32 * nt;
+                b[nt] = *reinterpret_cast<const v4i*>(L.wl[cur] + swz(r, 2 * ks + half));
             }
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const v4i a = __builtin_bit_cast(v4i, acur[mt][ks]);
+            for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    acch[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh[nt], acch[mt][nt], 0, 0, 0);
-                    accl[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl[nt], accl[mt][nt], 0, 0, 0);
-                }
-            }
+                for (int nt = 0; nt < NT; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt], acc[mt][nt], 0, 0, 0);
+            // this K step's A fragments are done: fetch those of super-block g+1
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+                afr[mt][ks] = __builtin_bit_cast(v4i, ld16(afrag[mt] + (int64_t)gn * 8192 + ks * 1024));
         }
 
-        // ---- epilogue of this super-block
+        // ---- epilogue of super-block g
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const int nl = 64 * wn + 32 * nt + l32;
-            const float d = sD[nl];
+        for (int mt = 0; mt < 2; mt++) {
+            f32x4 dxv[4];
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
+            for (int q = 0; q < 4; q++)
+                dxv[q] = *reinterpret_cast<const f32x4*>(&L.dx[cur][64 * wm + 32 * mt + 8 * q + 4 * half]);
+            const int ml = 64 * wm + 32 * mt + l32;
 #pragma unroll
-                for (int a = 0; a < 16; a++) {
-                    const int ml = 64 * wm + 32 * mt + (a >> 2) * 8 + half * 4 + (a & 3);
-                    const float dx = sDx[ml];
-                    const int i1 = (acch[mt][nt][a] << 7) + accl[mt][nt][a];
-                    yacc[mt][nt][a] = __builtin_fmaf(dx, __fmul_rn(d, (float)i1), yacc[mt][nt][a]);
+            for (int nt = 0; nt < NT; nt++) {
+                const int nl = nrow0 + 32 * nt;
+                const float dn = L.d[cur][nl];
+                if (TYPE == TYPE_Q4_K) {
+                    const float dmn = L.dm[cur][nl];
+                    const v8h bm = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&L.wmin[cur][nl * 8 + 4 * half]));
+                    const v8h am = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&L.xmin[cur][ml * 8 + 4 * half]));
+                    const v16f cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, v16f{}, 0, 0, 0);   // -I2
+#pragma unroll
+                    for (int a = 0; a < 16; a++) {
+                        const float t = __builtin_fmaf(dmn, cm[a], __fmul_rn(dn, (float)acc[mt][nt][a]));
+                        yacc[mt][nt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], t, yacc[mt][nt][a]);
+                    }
+                } else {
+#pragma unroll
+                    for (int a = 0; a < 16; a++)
+                        yacc[mt][nt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], __fmul_rn(dn, (float)acc[mt][nt][a]),
+                                                         yacc[mt][nt][a]);
                 }
             }
         }
@@ -371,8 +412,8 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
 
     // ---- store
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const int n = n0 + 64 * wn + 32 * nt + l32;
+    for (int nt = 0; nt < NT; nt++) {
+        const int n = n0 + nrow0 + 32 * nt;
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -383,14 +424,54 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     }
 }
 
+#ifndef KQ_GEMM_WN128
+#define KQ_GEMM_WN128 2   // waves along n for 128-row tiles
+#endif
+
+// Fragment-order copy of the activation quants (layout above); rows M .. 128*ceil(M/128)-1 are
+// zero.  One workgroup per (32-row tile, super-block), 32 bytes per thread.
+__global__ void __launch_bounds__(256)
+k_q8k_frag(const uint8_t* __restrict__ XQ, int M, int G, uint8_t* __restrict__ XF) {
+    const int mt = blockIdx.x, g = blockIdx.y;
+    uint8_t* out = XF + ((int64_t)mt * G + g) * 8192;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int t = threadIdx.x + 256 * j;            // 16-byte slot: ks = t / 64, lane = t % 64
+        const int ks = t >> 6, lane = t & 63;
+        const int row = 32 * mt + (lane & 31);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (row < M) v = ld16_a4(XQ + ((int64_t)row * G + g) * Q8K_BYTES + 4 + 32 * ks + 16 * (lane >> 5));
+        *reinterpret_cast<u32x4*>(out + 16 * t) = v;
+    }
+}
+
+size_t gemm_q8k_workspace(int C, int M) {
+    return (size_t)((M + GM_BM - 1) / GM_BM) * GM_BM * (size_t)C;
+}
+
+template <int TYPE, int BN, int WN>
+static void launch_tile(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
+                        int64_t ldy, hipStream_t s) {
+    dim3 grid((R + BN - 1) / BN, (M + GM_BM - 1) / GM_BM), block(128 * WN);
+    hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
+}
+
+template <int TYPE>
+static void launch_type(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
+                        int64_t ldy, hipStream_t s) {
+    // 128-row tiles when they give at least two workgroups per CU in total, else 64-row tiles
+    const int64_t tiles128 = (int64_t)((R + 127) / 128) * ((M + GM_BM - 1) / GM_BM);
+    if (tiles128 >= 2 * (int64_t)device_cus()) launch_tile<TYPE, 128, KQ_GEMM_WN128>(w, R, G, xq, xf, M, y, ldy, s);
+    else launch_tile<TYPE, 64, 2>(w, R, G, xq, xf, M, y, ldy, s);
+}
+
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
-                     hipStream_t s) {
+                     uint8_t* ws, hipStream_t s) {
     const int G = C / QK;
-    dim3 grid((R + GM_BN - 1) / GM_BN, (M + GM_BM - 1) / GM_BM), block(256);
-    if (type == TYPE_Q4_K)
-        hipLaunchKernelGGL(k_gemm_q8k<TYPE_Q4_K>, grid, block, 0, s, w, R, G, xq, M, y, ldy);
-    else
-        hipLaunchKernelGGL(k_gemm_q8k<TYPE_Q6_K>, grid, block, 0, s, w, R, G, xq, M, y, ldy);
+    dim3 fgrid((M + GM_BM - 1) / GM_BM * (GM_BM / 32), G);
+    hipLaunchKernelGGL(k_q8k_frag, fgrid, dim3(256), 0, s, xq, M, G, ws);
+    if (type == TYPE_Q4_K) launch_type<TYPE_Q4_K>(w, R, G, xq, ws, M, y, ldy, s);
+    else launch_type<TYPE_Q6_K>(w, R, G, xq, ws, M, y, ldy, s);
 }
 
 }  // namespace kq

@@ -362,18 +362,6 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
 }
 
 // ------------------------------------------------------------------ launch
-static int device_cus() {
-    static int cus[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
 // Rows per wave: 2 keeps per-wave register use moderate and gives many units to balance;
 // with several tokens per launch the register budget is NT*RPW <= 8 outputs per lane.
 static int pick_rpw(int nt) {

@@ -18,6 +18,9 @@ int check_ptr(const void* p, size_t align, const char* what, const char* fn);
 // Reports a failed launch (hipGetLastError) as KQ_ERR_HIP.
 int check_launch(const char* fn);
 
+// Compute units of the current device (cached per device).
+int device_cus();
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline int block_bytes(int type) { return type == KQ_TYPE_Q4_K ? 144 : 210; }
 
@@ -28,8 +31,10 @@ void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq
 // n (1..3) matrices of one type sharing xq; one launch per group of up to 4 tokens.
 void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s);
+// Prefill GEMM; ws holds gemm_q8k_workspace(C, M) bytes (16-byte aligned) of activation fragments.
+size_t gemm_q8k_workspace(int C, int M);
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
-                     hipStream_t s);
+                     uint8_t* ws, hipStream_t s);
 void launch_subblock_sums(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N,
                           int32_t* sums, hipStream_t s);
 void launch_gemv_f32(const uint8_t* w, int R, int C, int type, const float* x, float* y,

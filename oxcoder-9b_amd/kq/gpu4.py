@@ -55,6 +55,7 @@ class Engine:
         self.max_rows = max_rows
         # Q8_K workspace, preallocated like the reference's device scratch (gpu4.py:70-79).
         self.xq = torch.empty(max_rows * (cols // QK) * Q8K_BYTES, dtype=torch.uint8, device=self.device)
+        self.gemm_ws = None   # activation-fragment workspace of the prefill GEMM, grown on demand
 
     def _check_out(self, y, R, N=1):
         need = (N - 1) * (y.stride(0) if y.dim() == 2 else R) + R
@@ -101,15 +102,18 @@ class Engine:
         return 1
 
     def gemm(self, names, X, outs):
-        """Prefill GEMM over M rows of X [M][C]."""
+        """Prefill GEMM over M rows of X [M][C] (M <= max_rows of the engine workspace)."""
         M, C = X.shape
         xq = self._quantize(X, C)
+        need = ops.gemm_workspace_bytes(C, M) + 256
+        if self.gemm_ws is None or self.gemm_ws.numel() < need:
+            self.gemm_ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         for name, y in zip(names, outs):
             w, R, C_, ty = self.w[name]
             if C_ != C:
                 raise ValueError("column count mismatch for " + name)
             self._check_out(y, R, M)
-            ops.gemm_q8k(w, R, C_, ty, xq, M, y, y.stride(0))
+            ops.gemm_q8k(w, R, C_, ty, xq, M, y, y.stride(0), ws=self.gemm_ws)
         return 1
 
     def dequant(self, name, row, out=None):

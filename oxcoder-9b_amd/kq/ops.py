@@ -99,14 +99,38 @@ def gemv_q8k_multi(mats, xq, N, ys):
     return ys
 
 
-def gemm_q8k(w, R, C_, ty, xq, M, y, ldy=None):
-    """Y[m][r] for M Q8_K activation rows (kq_gemm_q8k, prefill)."""
+def gemm_workspace_bytes(C_, M):
+    """Device bytes of the activation-fragment workspace a prefill GEMM of M rows x C_ needs."""
+    return int(_lib.kq().kq_gemm_q8k_workspace(C_, M))
+
+
+def gemm_workspace(C_, M, device):
+    """A workspace tensor for gemm_q8k (kq_gemm_q8k_workspace bytes, 256-byte aligned)."""
+    return torch.empty(gemm_workspace_bytes(C_, M) + 256, dtype=torch.uint8, device=device)
+
+
+def _aligned(ws, n):
+    off = (-ws.data_ptr()) % 256
+    if ws.numel() - off < n:
+        raise ValueError("workspace holds %d usable bytes, %d needed" % (ws.numel() - off, n))
+    return C.c_void_p(ws.data_ptr() + off), ws.numel() - off
+
+
+def gemm_q8k(w, R, C_, ty, xq, M, y, ldy=None, ws=None):
+    """Y[m][r] for M Q8_K activation rows (prefill).  With ``ws`` (a device uint8 tensor of at least
+    gemm_workspace_bytes + 256 bytes) this is kq_gemm_q8k_ws and allocates nothing; without it,
+    kq_gemm_q8k with the library's per-stream workspace."""
     pw = _weights(w, R, C_, ty)
     ldy = R if ldy is None else ldy
     if xq.numel() < M * (C_ // QK) * Q8K_BYTES or y.numel() < (M - 1) * ldy + R:
         raise ValueError("xq or y too small")
-    _lib.check(_lib.kq().kq_gemm_q8k(pw, R, C_, ty, _dev(xq, "xq", torch.uint8), M,
-                                     _dev(y, "y", torch.float32), ldy, _stream(w.device)))
+    px, py, st = _dev(xq, "xq", torch.uint8), _dev(y, "y", torch.float32), _stream(w.device)
+    if ws is None:
+        _lib.check(_lib.kq().kq_gemm_q8k(pw, R, C_, ty, px, M, py, ldy, st))
+    else:
+        _dev(ws, "ws", torch.uint8)
+        pws, nws = _aligned(ws, gemm_workspace_bytes(C_, M))
+        _lib.check(_lib.kq().kq_gemm_q8k_ws(pw, R, C_, ty, px, M, py, ldy, pws, nws, st))
     return y
 
 

@@ -4,12 +4,14 @@ Bars: decode, Q8_K bytes and integer sub-block sums bit-exact; fp32 outputs with
 1e-5 * max|y_ref| (y_ref = oracle evaluated in double from the exact integer sums); batched rows
 bit-identical to the single-token result.
 """
+import ctypes as ct
+
 import numpy as np
 import pytest
 import torch
 
 from helpers import reference_unit_inputs
-from kq import ops, quantize as kqq
+from kq import _lib, ops, quantize as kqq
 from kq.formats import Q4_K, Q6_K
 
 pytestmark = pytest.mark.gpu
@@ -219,6 +221,43 @@ def test_gemm_q8k_reference_inputs(dev, orc, ty):
     y = torch.empty((37, R), device=dev)
     ops.gemm_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), 37, y)
     assert_close_inf(host(y), orc.gemv_q8k(W, R, C, ty, xq, 37))
+
+
+@pytest.mark.parametrize("ty", [12, 14])
+def test_gemm_q8k_ws_matches_cached_workspace(dev, orc, ty):
+    """kq_gemm_q8k_ws (caller workspace, shared by two calls of different M) equals kq_gemm_q8k
+    bit for bit, and both equal the oracle within the bar."""
+    R, C = 264, 1024
+    W = synth(R, C, ty, 41)
+    wd = dev_t(W, dev)
+    ws = ops.gemm_workspace(C, 300, dev)
+    for M in (300, 77):
+        xq = orc.quantize_q8k(kqq.synthetic_activations(M, C, seed=900 + M))
+        xqd = dev_t(xq, dev)
+        y_ws = torch.full((M, R), -1.0, device=dev)
+        y_lib = torch.full((M, R), -2.0, device=dev)
+        ops.gemm_q8k(wd, R, C, ty, xqd, M, y_ws, ws=ws)
+        ops.gemm_q8k(wd, R, C, ty, xqd, M, y_lib)
+        np.testing.assert_array_equal(host(y_ws), host(y_lib))
+        assert_close_inf(host(y_ws), orc.gemv_q8k(W, R, C, ty, xq, M))
+
+
+def test_gemm_q8k_ws_rejects_small_or_misaligned_workspace(dev):
+    R, C, M = 64, 512, 130
+    w = dev_t(synth(R, C, 12, 5), dev)
+    xq = torch.zeros(M * (C // 256) * 292, dtype=torch.uint8, device=dev)
+    y = torch.empty((M, R), device=dev)
+    need = ops.gemm_workspace_bytes(C, M)
+    assert need == 256 * C          # M rounded up to 128 rows, one byte per quant
+    small = torch.empty(need, dtype=torch.uint8, device=dev)
+    lib = _lib.kq()
+    args = lambda ws, n: (ct.c_void_p(w.data_ptr()), R, C, 12, ct.c_void_p(xq.data_ptr()), M,
+                          ct.c_void_p(y.data_ptr()), R, ws, n, None)
+    base = small.data_ptr() + (-small.data_ptr()) % 256
+    assert lib.kq_gemm_q8k_ws(*args(ct.c_void_p(base), need - 256)) == -1
+    assert b"workspace" in lib.kq_last_error()
+    assert lib.kq_gemm_q8k_ws(*args(ct.c_void_p(base + 16), need)) == -1
+    assert b"aligned" in lib.kq_last_error()
 
 
 # ------------------------------------------------------------------------------- fp32-x GEMV

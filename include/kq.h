@@ -87,11 +87,7 @@ int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const in
  * Prefill GEMM: Y[m][r] for M >= 1 activation rows (row stride ldy), int8 products with int32
  * accumulation and the fp32 epilogue above.  Slot of the ternary engine's chunk GEMM
  * k_mm_g5q (chunk.cu:820) driven by chunk.feed (chunk.py:378); the Q4 engine itself prefills
- * token by token (gpu4.py:109-110).  The call first copies the activation quants into a device
- * workspace in MFMA fragment order (about M*C bytes, M rounded up to 128), kept by the library per
- * (device, stream) and reused; a call that needs a larger workspace than the stream has allocates
- * one (hipMalloc, after a device synchronisation) and is refused with KQ_ERR_ARG while the
- * stream is capturing a graph, so capture a GEMM only after one call of at least that size.
+ * token by token (gpu4.py:109-110).  Allocates nothing; kq_gemm_q8k_ws below is the faster form.
  */
 int kq_gemm_q8k(const void* w, int R, int C, int type, const void* xq, int M, float* y,
                 int64_t ldy, void* stream);
@@ -101,8 +97,10 @@ size_t kq_gemm_q8k_workspace(int C, int M);
 
 /*
  * kq_gemm_q8k with a caller-provided workspace (ws 256-byte aligned, ws_bytes at least
- * kq_gemm_q8k_workspace(C, M)); allocates nothing, so it can be captured into a graph at any size.
- * Calls that share a workspace must be ordered (same stream or synchronised).
+ * kq_gemm_q8k_workspace(C, M), about M*C bytes with M rounded up to 128).  The call first copies
+ * the activation quants into ws in MFMA fragment order, so that every operand load of the GEMM is
+ * one contiguous 1 KB.  Allocates nothing; calls sharing a workspace must be ordered (same stream
+ * or synchronised).
  */
 int kq_gemm_q8k_ws(const void* w, int R, int C, int type, const void* xq, int M, float* y,
                    int64_t ldy, void* ws, size_t ws_bytes, void* stream);

@@ -3,8 +3,6 @@
 #include <stdio.h>
 #include <string.h>
 
-#include <mutex>
-
 #include "kq_internal.h"
 
 namespace kq {
@@ -155,56 +153,6 @@ int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const in
     return check_launch(fn);
 }
 
-// Workspace of kq_gemm_q8k (activation fragments), cached per (device, stream) so that calls on
-// different streams never share one.  It grows by reallocation after a device synchronisation;
-// growth is refused while the stream is being captured into a graph.
-namespace {
-struct GemmWs { int dev; void* stream; uint8_t* ptr; size_t bytes; uint64_t last; };
-std::mutex g_ws_mu;
-GemmWs g_ws[16];
-uint64_t g_ws_clock = 0;
-}  // namespace
-
-static int gemm_workspace(void* stream, size_t need, uint8_t** out, const char* fn) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return fail(KQ_ERR_HIP, "%s: hipGetDevice failed", fn);
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    GemmWs* slot = nullptr;
-    for (GemmWs& e : g_ws)
-        if (e.ptr && e.dev == dev && e.stream == stream) slot = &e;
-    if (slot && slot->bytes >= need) {
-        slot->last = ++g_ws_clock;
-        *out = slot->ptr;
-        return KQ_OK;
-    }
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(as_stream(stream), &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
-        return fail(KQ_ERR_ARG, "%s: the %zu-byte workspace for this stream must be created by a call outside "
-                    "graph capture first", fn, need);
-    if (!slot) {   // a free slot, else the least recently used one
-        slot = &g_ws[0];
-        for (GemmWs& e : g_ws) {
-            if (!e.ptr) { slot = &e; break; }
-            if (e.last < slot->last) slot = &e;
-        }
-    }
-    if (slot->ptr) {
-        int cur = dev;
-        if (hipSetDevice(slot->dev) != hipSuccess || hipDeviceSynchronize() != hipSuccess || hipFree(slot->ptr) != hipSuccess) {
-            (void)hipSetDevice(cur);
-            return fail(KQ_ERR_HIP, "%s: releasing a workspace failed", fn);
-        }
-        (void)hipSetDevice(cur);
-        slot->ptr = nullptr;
-    }
-    const size_t bytes = (need + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-    void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) return fail(KQ_ERR_HIP, "%s: hipMalloc(%zu) failed", fn, bytes);
-    *slot = GemmWs{dev, stream, static_cast<uint8_t*>(p), bytes, ++g_ws_clock};
-    *out = slot->ptr;
-    return KQ_OK;
-}
-
 static int check_gemm(const void* w, int R, int C, int type, const void* xq, int M, const float* y, int64_t ldy,
                       const char* fn) {
     KQ_TRY(check_matrix(w, R, C, type, fn));
@@ -220,10 +168,8 @@ int kq_gemm_q8k(const void* w, int R, int C, int type, const void* xq, int M, fl
                 int64_t ldy, void* stream) {
     static const char* fn = "kq_gemm_q8k";
     KQ_TRY(check_gemm(w, R, C, type, xq, M, y, ldy, fn));
-    uint8_t* ws = nullptr;
-    KQ_TRY(gemm_workspace(stream, gemm_q8k_workspace(C, M), &ws, fn));
-    launch_gemm_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), M, y, ldy, ws,
-                    as_stream(stream));
+    launch_gemm_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), M, y, ldy,
+                    nullptr, as_stream(stream));
     return check_launch(fn);
 }
 

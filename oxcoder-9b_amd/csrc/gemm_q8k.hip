@@ -28,9 +28,11 @@
 // it straight from Q8_K rows touches 32-64 cache lines per load instruction, for every weight
 // tile.  A first pass (k_q8k_frag) rewrites the quants once into fragment order,
 //   frag[m/32][g][ks 0..7][lane 0..63][16 B] = qs bytes 32ks + 16(lane/32) .. +15 of row 32(m/32) + lane%32,
-// so each A load is one contiguous 1 KB; rows are padded to a multiple of 128 with zeros.  The
-// next super-block's raw weight bytes and activation fragments are loaded one step ahead.  Rows
-// past R are clamped for loading and not stored.
+// so each A load is one contiguous 1 KB; rows are padded to a multiple of 128 with zeros.  This
+// needs a caller workspace (kq_gemm_q8k_ws); without one (kq_gemm_q8k, which allocates nothing)
+// the fragments are read from the Q8_K rows directly.  The next super-block's raw weight bytes
+// and activation fragments are loaded one step ahead.  Rows past M or R are clamped for loading
+// and not stored.
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -259,7 +261,8 @@ __device__ __forceinline__ void stage_x(const RawX<XP>& r, int mr, int xp, GemmL
 
 // ------------------------------------------------------------------ the kernel
 // WN waves along n (2 or 4) times 2 along m; each wave owns 64 tokens x BN/WN weight rows.
-template <int TYPE, int BN, int WN>
+// FRAG: A operands from the fragment-order copy XF, else straight from the Q8_K rows XQ.
+template <int TYPE, int BN, int WN, bool FRAG>
 __global__ void __launch_bounds__(128 * WN)
 k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restrict__ XQ,
            const uint8_t* __restrict__ XF, int M, float* __restrict__ Y, int64_t ldy) {
@@ -280,11 +283,19 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * GM_BM;
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
 
-    // A operand fragments of this lane: tile (m0 + 64 wm + 32 mt) / 32, 8 KB per super-block
+    // A operand of this lane for K step ks of super-block g: afrag[mt] + g * AG + ks * AK
+    constexpr int AG = FRAG ? 8192 : Q8K_BYTES, AK = FRAG ? 1024 : 32;
     const uint8_t* afrag[2];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
-        afrag[mt] = XF + ((int64_t)(blockIdx.y * 4 + 2 * wm + mt) * G * 512 + lane) * 16;
+    for (int mt = 0; mt < 2; mt++) {
+        if (FRAG) {   // fragment tile (m0 + 64 wm + 32 mt) / 32
+            afrag[mt] = XF + ((int64_t)(blockIdx.y * 4 + 2 * wm + mt) * G * 512 + lane) * 16;
+        } else {      // row m, bytes 32 ks + 16 half of its quants
+            int m = m0 + 64 * wm + 32 * mt + l32;
+            m = m < M ? m : M - 1;
+            afrag[mt] = XQ + m * xrow + 4 + 16 * half;
+        }
+    }
     // activation row staged by this thread
     const int mr = tid & 127, xp = tid >> 7;
     const uint8_t* xstage = XQ + (int64_t)(m0 + mr < M ? m0 + mr : M - 1) * xrow;
@@ -310,7 +321,7 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) afr[mt][ks] = __builtin_bit_cast(v4i, ld16(afrag[mt] + ks * 1024));
+        for (int ks = 0; ks < 8; ks++) afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + ks * AK));
     unpack(raw, pi, prow, L, 0);
     stage_x<TYPE>(rx, mr, xp, L, 0);
     {
@@ -374,7 +385,7 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
             // this K step's A fragments are done: fetch those of super-block g+1
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
-                afr[mt][ks] = __builtin_bit_cast(v4i, ld16(afrag[mt] + (int64_t)gn * 8192 + ks * 1024));
+                afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
         }
 
         // ---- epilogue of super-block g
@@ -453,7 +464,8 @@ template <int TYPE, int BN, int WN>
 static void launch_tile(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
                         int64_t ldy, hipStream_t s) {
     dim3 grid((R + BN - 1) / BN, (M + GM_BM - 1) / GM_BM), block(128 * WN);
-    hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
+    if (xf) hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, true>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
+    else hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, false>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
 }
 
 template <int TYPE>
@@ -468,8 +480,10 @@ static void launch_type(const uint8_t* w, int R, int G, const uint8_t* xq, const
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
                      uint8_t* ws, hipStream_t s) {
     const int G = C / QK;
-    dim3 fgrid((M + GM_BM - 1) / GM_BM * (GM_BM / 32), G);
-    hipLaunchKernelGGL(k_q8k_frag, fgrid, dim3(256), 0, s, xq, M, G, ws);
+    if (ws) {
+        dim3 fgrid((M + GM_BM - 1) / GM_BM * (GM_BM / 32), G);
+        hipLaunchKernelGGL(k_q8k_frag, fgrid, dim3(256), 0, s, xq, M, G, ws);
+    }
     if (type == TYPE_Q4_K) launch_type<TYPE_Q4_K>(w, R, G, xq, ws, M, y, ldy, s);
     else launch_type<TYPE_Q6_K>(w, R, G, xq, ws, M, y, ldy, s);
 }

@@ -31,7 +31,8 @@ void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq
 // n (1..3) matrices of one type sharing xq; one launch per group of up to 4 tokens.
 void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s);
-// Prefill GEMM; ws holds gemm_q8k_workspace(C, M) bytes (16-byte aligned) of activation fragments.
+// Prefill GEMM; ws (or nullptr) holds gemm_q8k_workspace(C, M) bytes (16-byte aligned) for the
+// activation fragments.
 size_t gemm_q8k_workspace(int C, int M);
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
                      uint8_t* ws, hipStream_t s);

@@ -118,8 +118,8 @@ def _aligned(ws, n):
 
 def gemm_q8k(w, R, C_, ty, xq, M, y, ldy=None, ws=None):
     """Y[m][r] for M Q8_K activation rows (prefill).  With ``ws`` (a device uint8 tensor of at least
-    gemm_workspace_bytes + 256 bytes) this is kq_gemm_q8k_ws and allocates nothing; without it,
-    kq_gemm_q8k with the library's per-stream workspace."""
+    gemm_workspace_bytes + 256 bytes) this is the faster kq_gemm_q8k_ws; without it, kq_gemm_q8k
+    (operands read straight from the Q8_K rows).  Neither allocates."""
     pw = _weights(w, R, C_, ty)
     ldy = R if ldy is None else ldy
     if xq.numel() < M * (C_ // QK) * Q8K_BYTES or y.numel() < (M - 1) * ldy + R:

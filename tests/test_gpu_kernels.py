@@ -210,6 +210,12 @@ def test_gemm_q8k_vs_oracle(dev, orc, ty, R, C, M):
     got = host(y)
     assert np.all(got[:, R:] == -3.0)
     assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C, ty, xq, M))
+    # the fragment-order path (caller workspace) gives the same bits
+    y2 = torch.full((M, R + 8), -4.0, device=dev)
+    ops.gemm_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), M, y2, R + 8, ws=ops.gemm_workspace(C, M, dev))
+    got2 = host(y2)
+    np.testing.assert_array_equal(got2[:, :R], got[:, :R])
+    assert np.all(got2[:, R:] == -4.0)
 
 
 @pytest.mark.parametrize("ty", [12, 14])
@@ -224,9 +230,9 @@ def test_gemm_q8k_reference_inputs(dev, orc, ty):
 
 
 @pytest.mark.parametrize("ty", [12, 14])
-def test_gemm_q8k_ws_matches_cached_workspace(dev, orc, ty):
+def test_gemm_q8k_ws_matches_direct(dev, orc, ty):
     """kq_gemm_q8k_ws (caller workspace, shared by two calls of different M) equals kq_gemm_q8k
-    bit for bit, and both equal the oracle within the bar."""
+    (operands straight from the Q8_K rows) bit for bit, and both equal the oracle within the bar."""
     R, C = 264, 1024
     W = synth(R, C, ty, 41)
     wd = dev_t(W, dev)

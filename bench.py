@@ -144,11 +144,7 @@ def kernel_roofline(torch, rn, layers, xqs, ys, repeats=5):
     A graph holds those launches for every resident layer copy back to back; HIP events around
     its replays on the launch stream give the mean launch duration (inter-launch gaps
     included).  Returns (mean algorithmic bytes per launch, mean seconds per launch, launches)."""
-    groups = []
-    for slot, C_ in enumerate(INPUT_COLS):
-        g = [(n, R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == slot]
-        if all(ty == 12 for *_, ty in g):
-            groups.append((slot, g))
+    groups = roofline_groups()
 
     def fn():
         s = rn.stream()
@@ -162,6 +158,44 @@ def kernel_roofline(torch, rn, layers, xqs, ys, repeats=5):
     launches = repeats * len(layers) * len(groups)
     nbytes = [sum(wbytes(R, C2, ty) + R * 4 for _, R, C2, ty in g) + (g[0][2] // 256) * Q8K for _, g in groups]
     return float(np.mean(nbytes)), el / launches, launches
+
+
+def roofline_groups():
+    groups = []
+    for slot, C_ in enumerate(INPUT_COLS):
+        g = [(n, R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == slot]
+        if all(ty == 12 for *_, ty in g):
+            groups.append((slot, g))
+    return groups
+
+
+def pmc_workload(torch, rn, layers, xs, xqs, ys, dev):
+    """The roofline kernel's launches (direct, no graph) over every resident layer copy, then a
+    64 MiB device-to-device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters."""
+    s = rn.stream()
+    for slot, g in roofline_groups():
+        rn.quantize(xs[slot], g[0][2], xqs[slot], s)
+    for layer in layers:
+        for slot, g in roofline_groups():
+            rn.gemv_multi([(layer[n], R, C2, ty) for n, R, C2, ty in g], xqs[slot], [ys[n] for n, *_ in g], s)
+    src = torch.ones(1 << 24, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log("pmc workload: %d GEMV launches, one 64 MiB copy" % (len(layers) * len(roofline_groups())))
+
+
+def traffic_from_profile(path=os.path.join(ROOT, "profiles", "gemv_q4k_decode_layer_traffic.md")):
+    """HBM bytes per launch of the roofline kernel as recorded by the committed counter summary
+    (line 'traffic_bytes_per_launch = N'), or None when the summary is absent."""
+    try:
+        for line in open(path):
+            if line.strip().startswith("traffic_bytes_per_launch"):
+                return int(float(line.split("=")[1]))
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline(budget_s=12.0):
@@ -291,6 +325,9 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="no timing: launch the roofline kernel's workload once per layer copy, then one "
+                         "64 MiB device copy (the calibration kernel), for rocprofv3 --pmc runs")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the products shard by "
@@ -305,8 +342,12 @@ def main():
     layers = make_layer(torch, dev, a.copies)
     from kq import quantize as kqq
     xs = [torch.from_numpy(kqq.synthetic_activations(1, c, seed=s)[0]).to(dev) for s, c in enumerate(INPUT_COLS)]
-    xqs = [torch.empty((c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
     ys = {name: torch.empty(R, device=dev) for name, R, _, _, _ in LAYER}
+
+    xqs = [torch.empty((c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
+    if a.pmc_workload:
+        pmc_workload(torch, rn, layers, xs, xqs, ys, dev)
+        return
 
     def steps(n, start=0):
         def fn():
@@ -340,8 +381,8 @@ def main():
                    "bytes_per_step": nbytes, "resident_layer_copies": a.copies,
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv_q8k<12,1,2,true> (Q4_K x Q8_K GEMV: q+k+v, o, gate+up launches)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "kernel": "k_gemv_q8k_split<12,1,2> (Q4_K x Q8_K GEMV: q+k+v, o, gate+up launches)",
                      "launches": kn,
                      "avg_bytes_per_launch": round(kb), "avg_us_per_launch": round(ks * 1e6, 3)},
     }

@@ -253,8 +253,9 @@ def batched_extra(torch, rn, dev, steps):
     return out
 
 
-def gemm_extra(torch, rn, dev):
-    """Prefill GEMM: M in {512, 2048}; 12288x4096 Q4_K and 4096x12288 Q6_K."""
+def gemm_extra(torch, rn, dev, timed=True):
+    """Prefill GEMM: M in {512, 2048}; 12288x4096 Q4_K and 4096x12288 Q6_K (timed=False: two
+    direct calls per shape, for counter runs)."""
     from kq import ops, quantize as kqq
     out = {}
     for name, R, C_, ty in (("gate_12288x4096_q4k", 12288, 4096, 12), ("down_4096x12288_q6k", 4096, 12288, 14)):
@@ -264,6 +265,11 @@ def gemm_extra(torch, rn, dev):
             xq = ops.q8k_quantize(X)
             y = torch.empty((M, R), device=dev)
             ws = torch.empty(ops.gemm_workspace_bytes(C_, M), dtype=torch.uint8, device=dev)
+            if not timed:
+                for _ in range(2):
+                    rn.gemm(w, R, C_, ty, xq, M, y, ws, rn.stream())
+                torch.cuda.synchronize()
+                continue
             g = capture(torch, lambda: rn.gemm(w, R, C_, ty, xq, M, y, ws, rn.stream()))
             time_graphs(torch, [g])
             reps = 3
@@ -325,9 +331,10 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="no timing: launch the roofline kernel's workload once per layer copy, then one "
-                         "64 MiB device copy (the calibration kernel), for rocprofv3 --pmc runs")
+    ap.add_argument("--pmc-workload", choices=("gemv", "gemm"),
+                    help="no timing, for rocprofv3 --pmc runs: 'gemv' launches the roofline kernel's "
+                         "workload once per layer copy, then one 64 MiB device copy (the calibration "
+                         "kernel); 'gemm' runs each prefill GEMM shape twice")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the products shard by "
@@ -338,6 +345,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     rn = Runner(torch)
+    if a.pmc_workload == "gemm":
+        gemm_extra(torch, rn, dev, timed=False)
+        return
     log("bench: building %d resident layer copies" % a.copies)
     layers = make_layer(torch, dev, a.copies)
     from kq import quantize as kqq
@@ -345,7 +355,7 @@ def main():
     ys = {name: torch.empty(R, device=dev) for name, R, _, _, _ in LAYER}
 
     xqs = [torch.empty((c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
-    if a.pmc_workload:
+    if a.pmc_workload == "gemv":
         pmc_workload(torch, rn, layers, xs, xqs, ys, dev)
         return
 

@@ -20,6 +20,15 @@
 #ifndef KQ_GEMV_WAVES_PER_CU
 #define KQ_GEMV_WAVES_PER_CU 8
 #endif
+#ifndef KQ_GEMV_WAVES_PER_CU_Q6
+#define KQ_GEMV_WAVES_PER_CU_Q6 KQ_GEMV_WAVES_PER_CU
+#endif
+#ifndef KQ_GEMV_SPLIT_MAX
+#define KQ_GEMV_SPLIT_MAX 4      // most column passes handled by the pass-split kernel (Q4_K)
+#endif
+#ifndef KQ_GEMV_SPLIT_MAX_Q6
+#define KQ_GEMV_SPLIT_MAX_Q6 2   // Q6_K: 3-4 passes run faster as sequential passes (measured)
+#endif
 #ifndef KQ_GEMV_WG_WAVES
 #define KQ_GEMV_WG_WAVES 4
 #endif
@@ -43,10 +52,11 @@ struct MatGroup {
 // ------------------------------------------------------------------ per-type fragments
 template <int TYPE> struct Frag;
 template <> struct Frag<TYPE_Q4_K> { u32x4 hdr, qa, qb; };
-// Q6_K fields sit at block offset + (block start & 3): the fragment holds the raw dword-aligned
-// words (each 16-B field + the following dword) and the byte shift; the funnel shift happens in
-// block_value so that issuing a prefetch never waits for its data.
-template <> struct Frag<TYPE_Q6_K> { u32x4 l0, l1, hb; uint32_t l0e, l1e, hbe; u32x2 sc; uint32_t sce, dw, sh; };
+// Q6_K fields sit at block offset + (block start & 3): a lane multiplies its dword-aligned words
+// (each 16-B field + the following dword), the scales and d, funnel-shifted by the byte shift in
+// block_value.
+struct Q6Fields { u32x4 l0, l1, hb; uint32_t l0e, l1e, hbe; u32x2 sc; uint32_t sce, dw, sh; };
+template <> struct Frag<TYPE_Q6_K> { Q6Fields f; };
 
 template <int TYPE> struct Act;
 template <> struct Act<TYPE_Q4_K> { uint32_t xl[8], xh[8]; int blo, bhi; float dx; };
@@ -62,7 +72,8 @@ __device__ __forceinline__ void load_frag(Frag<TYPE_Q4_K>& f, const uint8_t* bk,
 // the scale window [192 + 8h, 200 + 8h) and d [208, 210) are read from the dword-aligned address
 // at or below them; for even rows (block start = 0 mod 4) the last word read reaches 2 bytes
 // into the next row's block, which exists because row 7 of a tile is odd.
-__device__ __forceinline__ void load_frag(Frag<TYPE_Q6_K>& f, const uint8_t* bk, int p) {
+__device__ __forceinline__ void load_frag(Frag<TYPE_Q6_K>& fr, const uint8_t* bk, int p) {
+    Q6Fields& f = fr.f;
     const int h = p >> 1, jj = p & 1;
     // pointer arithmetic (not an integer round trip) keeps the global address space
     f.sh = uint32_t(reinterpret_cast<uintptr_t>(bk) & 3);   // the same shift for every field
@@ -77,6 +88,9 @@ __device__ __forceinline__ void load_frag(Frag<TYPE_Q6_K>& f, const uint8_t* bk,
     f.sce = ld4(b4 + 200 + 8 * h);
     f.dw = ld4(b4 + 208);
 }
+// The fields a lane multiplies (the fragment itself for both types).
+__device__ __forceinline__ const Q6Fields& prepare(const Frag<TYPE_Q6_K>& f) { return f.f; }
+__device__ __forceinline__ const Frag<TYPE_Q4_K>& prepare(const Frag<TYPE_Q4_K>& f) { return f; }
 __device__ __forceinline__ u32x4 funnel(const u32x4& v, uint32_t e, uint32_t sh) {
     u32x4 r;
     r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
@@ -122,7 +136,7 @@ __device__ __forceinline__ float block_value(const Frag<TYPE_Q4_K>& f, const Act
     const int i2 = quad_sum_i32((int)sm.m_lo * a.blo + (int)sm.m_hi * a.bhi);
     return q4k_value(f.hdr.x, a.dx, i1, i2);
 }
-__device__ __forceinline__ float block_value(const Frag<TYPE_Q6_K>& f, const Act<TYPE_Q6_K>& a, int p) {
+__device__ __forceinline__ float block_value(const Q6Fields& f, const Act<TYPE_Q6_K>& a, int p) {
     const int jj = p & 1;
     const uint32_t w0 = __builtin_amdgcn_alignbyte(f.sc.y, f.sc.x, f.sh);   // scales 8h .. 8h+3
     const uint32_t w1 = __builtin_amdgcn_alignbyte(f.sce, f.sc.y, f.sh);    // scales 8h+4 .. 8h+7
@@ -214,12 +228,14 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
             for (int t = 0; t < NT; t++) load_act(act[t], XQ + ((int64_t)t * G + gc) * Q8K_BYTES, p);
         }
 #pragma unroll
-        for (int t = 0; t < NT; t++)
+        for (int r = 0; r < RPW; r++) {
+            const auto& fr = prepare(cur[r]);
 #pragma unroll
-            for (int r = 0; r < RPW; r++) {
-                const float v = block_value(cur[r], act[t], p);
+            for (int t = 0; t < NT; t++) {
+                const float v = block_value(fr, act[t], p);
                 tree_push(tree[t][r], slot_tree_f32(valid ? v : 0.0f));
             }
+        }
 
         if (pass == passes - 1) {
 #pragma unroll
@@ -315,10 +331,11 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
             // keep every prefetch load ahead of this step's compute (and its waits)
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int t = 0; t < NT; t++)
+            for (int r = 0; r < RPW; r++) {
+                const auto& fr = prepare(cur[r]);
 #pragma unroll
-                for (int r = 0; r < RPW; r++) {
-                    const float v = block_value(cur[r], act[t], p);
+                for (int t = 0; t < NT; t++) {
+                    const float v = block_value(fr, act[t], p);
                     const float pv = slot_tree_f32(valid ? v : 0.0f);
                     if (P == 1) {
                         if (lane == 0) mg.y[m][t * mg.ldy[m] + row0 + r] = __fadd_rn(pv, 0.0f);
@@ -326,6 +343,7 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
                         mypart[((k * NT + t) * RPW + r) * P + pass] = pv;
                     }
                 }
+            }
             if (!has_next) return false;
             u = un; k++; m = mn; row0 = row0n; base = basen;
             return true;
@@ -364,7 +382,11 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
 // ------------------------------------------------------------------ launch
 // Rows per wave: 2 keeps per-wave register use moderate and gives many units to balance;
 // with several tokens per launch the register budget is NT*RPW <= 8 outputs per lane.
-static int pick_rpw(int nt) {
+static int pick_rpw(int nt, int type) {
+#ifdef KQ_GEMV_RPW_Q6
+    if (type == TYPE_Q6_K) return KQ_GEMV_RPW_Q6;
+#endif
+    (void)type;
 #ifdef KQ_GEMV_RPW
     (void)nt;
     return KQ_GEMV_RPW;
@@ -383,11 +405,12 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
     }
     mg.first_unit[3] = total;
     const int passes = (G + 15) / 16;
-    if (passes <= 4) {
+    const int wpc = TYPE == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_Q6 : KQ_GEMV_WAVES_PER_CU;
+    if (passes <= (TYPE == TYPE_Q6_K ? KQ_GEMV_SPLIT_MAX_Q6 : KQ_GEMV_SPLIT_MAX)) {
         // K unit streams of `passes` waves per workgroup (about KQ_GEMV_WG_WAVES waves per
         // workgroup); about KQ_GEMV_WAVES_PER_CU waves per CU in total
         const int K = passes >= KQ_GEMV_WG_WAVES ? 1 : KQ_GEMV_WG_WAVES / passes;
-        int streams = device_cus() * KQ_GEMV_WAVES_PER_CU / passes;
+        int streams = device_cus() * wpc / passes;
         if (streams > total) streams = total;
         auto round_xcd = [](int n) { return (n + KQ_XCDS - 1) / KQ_XCDS * KQ_XCDS; };
         int nwg = round_xcd((streams + K - 1) / K);
@@ -406,7 +429,7 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
         return;
     }
     const int wpb = 4;
-    int waves = device_cus() * KQ_GEMV_WAVES_PER_CU;
+    int waves = device_cus() * wpc;
     if (waves > total) waves = total;
     dim3 grid((waves + wpb - 1) / wpb), block(64 * wpb);
     if (G <= 16)
@@ -455,8 +478,8 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
         }
         for (int i = n; i < 4; i++) mg.first_unit[i] = tiles;
         const uint8_t* xg = xq + (int64_t)n0 * G * Q8K_BYTES;
-        if (type == TYPE_Q4_K) launch1<TYPE_Q4_K>(mg, xg, G, nt, pick_rpw(nt), s);
-        else launch1<TYPE_Q6_K>(mg, xg, G, nt, pick_rpw(nt), s);
+        if (type == TYPE_Q4_K) launch1<TYPE_Q4_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q4_K), s);
+        else launch1<TYPE_Q6_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q6_K), s);
     }
 }
 

@@ -20,15 +20,15 @@ OBJ = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["api.hip", "q8k_quantize.hip", "gemv_q8k.hip", "gemv_f32.hip", "gemm_q8k.hip"]
+HIP_SOURCES = ["api.hip", "q8k_quantize.hip", "gemv_q8k.hip", "gemv_mfma.hip", "gemv_f32.hip", "gemm_q8k.hip"]
 HIP_FLAGS = [
     "--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-I" + CSRC, "-I" + os.path.join(ROOT, "include"),
 ]
-# Per-source extra flags.  The GEMM keeps its MFMA accumulators in ordinary VGPRs (the epilogue
+# Per-source extra flags.  The MFMA kernels keep their accumulators in ordinary VGPRs (the epilogue
 # reads them with VALU instructions every super-block; accumulators in AGPRs would need a copy each).
-HIP_EXTRA = {"gemm_q8k.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+HIP_EXTRA = {"gemm_q8k.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HOST_SOURCES = ["host/quantize_weights.cpp"]
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
               "-fno-math-errno", "-Wall", "-I" + os.path.join(ROOT, "include")]

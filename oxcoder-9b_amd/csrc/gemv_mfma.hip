@@ -1,0 +1,292 @@
+// Small-batch GEMV (speculative verify, 3..16 tokens) on int8 MFMA for gfx950.
+//
+// A wave owns 16 weight rows x 4 consecutive super-blocks (a "chunk") for all tokens: per
+// super-block it forms the exact integers of the GEMV (Q4_K: I1 = sum sc_s*S_s and
+// I2 = sum m_s*B_s; Q6_K: I = sum sc_t*(S_t - 32*b_t)) with v_mfma_i32_16x16x64_i8 (tokens x rows,
+// K = 64 per step), turns them into the per-super-block fp32 value with the GEMV's own formula
+// (q4k_value / q6k_value) and adds the chunk's four values as ((v0+v1)+(v2+v3)).  A workgroup
+// holds every chunk of its 16 rows; after one barrier the chunk sums of each 16-column pass are
+// merged as ((c0+c1)+(c2+c3)) and the passes with the pass tree, which is exactly the column tree
+// of the GEMV (zero-padded columns included).  Every output is therefore bit-identical to the
+// GEMV of that token alone.
+//
+// Operands.  The scale is folded into the weights as in the prefill GEMM, split into two int8
+// planes: Q4_K sc = 8a + b, planes a*q and b*q (I1 = 8*(x.H) + (x.L)); Q6_K w = sc*(q - 32),
+// v = w + 128, planes high byte of v and low byte of v ^ 0x80 (I = 256*(x.H) + (x.L)).  The Q4_K
+// min term is one v_mfma_f32_16x16x16_f16 with exact small-integer operands [B_s >> 6, B_s & 63]
+// and [-64 m_s, -m_s], which returns -I2 exactly.
+//
+// MFMA lanes: lane l serves token (A operand) and weight row (B operand) l & 15 and K chunk
+// q = l >> 4 (16 bytes); K step p covers super-block elements 64p .. 64p+63, the lane's 16 are
+// 64p + 16q + i.  Outputs: lane l holds tokens 4q + j (j = 0..3) of row l & 15.
+#include "kq_device.h"
+#include "kq_internal.h"
+#include "q4_lanes.h"
+
+namespace kq {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int MV_ROWS = 16;     // weight rows per workgroup
+constexpr int MV_CHUNK = 4;     // super-blocks per wave
+
+struct MvGroup {
+    const uint8_t* w[3];
+    float* y[3];
+    int64_t ldy[3];
+    int R[3];
+    int first[4];   // workgroups of matrix m are [first[m], first[m+1])
+};
+
+__device__ __forceinline__ uint32_t mv_mul_u8x4(uint32_t q, uint32_t s2) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, s2));
+}
+__device__ __forceinline__ uint32_t mv_pk_f16(float a, float b) {   // exact small integers only
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
+// ------------------------------------------------------------------ per-super-block operands
+template <int TYPE> struct MvW;
+// Q4_K: header and, per K step p, the 16 qs bytes 32p + 16(q & 1) .. +15 (low nibbles for q < 2).
+template <> struct MvW<TYPE_Q4_K> { u32x4 hdr, qs[4]; };
+// Q6_K: dword-aligned raw words: ql bytes 64h + 16q (h = 0, 1), qh bytes 32h + 16(q & 1), the 16
+// scales and d, each 16-byte field with the dword after it; sh = block start & 3.
+template <> struct MvW<TYPE_Q6_K> { u32x4 ql[2], qh[2], sc; uint32_t qle[2], qhe[2], sce, sh; };
+
+struct MvX {
+    u32x4 a[4];     // activation bytes 64p + 16q .. +15 of token l & 15
+    u32x4 bs;       // bsums 8(q & 1) .. 8(q & 1) + 7 of token l & 15 (Q4_K min term)
+    float dx[4];    // d of tokens 4q + j
+};
+
+__device__ __forceinline__ void mv_load(MvW<TYPE_Q4_K>& w, const uint8_t* bk, int q) {
+    w.hdr = ld16(bk);
+#pragma unroll
+    for (int p = 0; p < 4; p++) w.qs[p] = ld16(bk + 16 + 32 * p + 16 * (q & 1));
+}
+// The last word read (bytes 208..211 from the aligned base) passes the block end by 2 bytes only
+// for blocks starting at 0 (mod 4), which are never row 7 of a tile column.
+__device__ __forceinline__ void mv_load(MvW<TYPE_Q6_K>& w, const uint8_t* bk, int q) {
+    w.sh = uint32_t(reinterpret_cast<uintptr_t>(bk) & 3);
+    const uint8_t* b4 = bk - w.sh;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        w.ql[h] = ld16_a4(b4 + 64 * h + 16 * q);
+        w.qle[h] = ld4(b4 + 64 * h + 16 * q + 16);
+        w.qh[h] = ld16_a4(b4 + 128 + 32 * h + 16 * (q & 1));
+        w.qhe[h] = ld4(b4 + 144 + 32 * h + 16 * (q & 1));
+    }
+    w.sc = ld16_a4(b4 + 192);
+    w.sce = ld4(b4 + 208);
+}
+// xa: Q8_K block of token l & 15; xd[j]: Q8_K block of token 4q + j (tokens clamped by the caller).
+__device__ __forceinline__ void mv_load_x(MvX& x, const uint8_t* xa, const uint8_t* const* xd, int q) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) x.a[p] = ld16_a4(xa + 4 + 64 * p + 16 * q);
+    x.bs = ld16_a4(xa + 260 + 16 * (q & 1));
+#pragma unroll
+    for (int j = 0; j < 4; j++) x.dx[j] = __builtin_bit_cast(float, ld4(xd[j]));
+}
+
+__device__ __forceinline__ u32x4 mv_funnel(const u32x4& v, uint32_t e, uint32_t sh) {
+    return u32x4{__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
+                 __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(e, v.w, sh)};
+}
+
+// The four per-super-block values (tokens 4q + j of row l & 15).
+__device__ __forceinline__ void mv_values(const MvW<TYPE_Q4_K>& w, const MvX& x, int q, float v[4]) {
+    v4i hp[4], lp[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const ScMin sm = q4k_scmin_pair(w.hdr.y, w.hdr.z, w.hdr.w, p);
+        const uint32_t sc = (q >> 1) ? sm.sc_hi : sm.sc_lo;          // sub-block 2p + (q >> 1)
+        const uint32_t a2 = (sc >> 3) * 0x10001u, b2 = (sc & 7u) * 0x10001u;
+        const uint32_t ws[4] = {w.qs[p].x, w.qs[p].y, w.qs[p].z, w.qs[p].w};
+        uint32_t hh[4], ll[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t nib = ((q >> 1) ? (ws[i] >> 4) : ws[i]) & 0x0f0f0f0fu;
+            hh[i] = mv_mul_u8x4(nib, a2);
+            ll[i] = mv_mul_u8x4(nib, b2);
+        }
+        hp[p] = v4i{(int)hh[0], (int)hh[1], (int)hh[2], (int)hh[3]};
+        lp[p] = v4i{(int)ll[0], (int)ll[1], (int)ll[2], (int)ll[3]};
+    }
+    v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[0]), hp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+    for (int p = 1; p < 4; p++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[p]), hp[p], acc, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[j] <<= 3;
+#pragma unroll
+    for (int p = 0; p < 4; p++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[p]), lp[p], acc, 0, 0, 0);
+
+    // min term: K 4q..4q+3 = sub-blocks 4(q & 1) .. +3, the high (q < 2) or low part of B
+    const ScMin m0 = q4k_scmin_pair(w.hdr.y, w.hdr.z, w.hdr.w, 2 * (q & 1));
+    const ScMin m1 = q4k_scmin_pair(w.hdr.y, w.hdr.z, w.hdr.w, 2 * (q & 1) + 1);
+    const float f = (q >> 1) ? -1.0f : -64.0f;
+    const v4h bm = __builtin_bit_cast(v4h, u32x2{mv_pk_f16(f * (float)m0.m_lo, f * (float)m0.m_hi),
+                                                 mv_pk_f16(f * (float)m1.m_lo, f * (float)m1.m_hi)});
+    const uint32_t bw[4] = {x.bs.x, x.bs.y, x.bs.z, x.bs.w};
+    float B[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int s = shalf(bw[k], 0) + shalf(bw[k], 1);
+        B[k] = (float)((q >> 1) ? (s & 63) : (s >> 6));
+    }
+    const v4h am = __builtin_bit_cast(v4h, u32x2{mv_pk_f16(B[0], B[1]), mv_pk_f16(B[2], B[3])});
+    const v4f cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);   // -I2
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = q4k_value(w.hdr.x, x.dx[j], acc[j], (int)(-cm[j]));
+}
+
+__device__ __forceinline__ void mv_values(const MvW<TYPE_Q6_K>& w, const MvX& x, int q, float v[4]) {
+    const uint32_t sh = w.sh;
+    u32x4 QL[2], QH[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        QL[h] = mv_funnel(w.ql[h], w.qle[h], sh);
+        QH[h] = mv_funnel(w.qh[h], w.qhe[h], sh);
+    }
+    const u32x4 SC = mv_funnel(w.sc, w.sce, sh);          // the 16 int8 scales
+    const float d = f16_lo(w.sce >> (8 * sh));             // bytes 208, 209 of the block
+    const uint32_t scw[4] = {SC.x, SC.y, SC.z, SC.w};
+    v4i hp[4], lp[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int h = p >> 1, k = 2 * (p & 1) + (q >> 1);
+        const int t = 8 * h + 2 * k + (q & 1);            // scale of elements 64p + 16q + i
+        const int sc = sbyte(scw[t >> 2], t & 3);
+        const s16x2 s2 = __builtin_bit_cast(s16x2, (uint32_t)(sc & 0xffff) * 0x10001u);
+        const s16x2 c2 = __builtin_bit_cast(s16x2, (uint32_t)((128 - 32 * sc) & 0xffff) * 0x10001u);
+        const uint32_t lw[4] = {QL[h].x, QL[h].y, QL[h].z, QL[h].w};
+        const uint32_t hw[4] = {QH[h].x, QH[h].y, QH[h].z, QH[h].w};
+        uint32_t hh[4], ll[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lq = (lw[i] >> (4 * (p & 1))) & 0x0f0f0f0fu;
+            const uint32_t hq = ((hw[i] >> (2 * k)) & 0x03030303u) << 4;
+            const uint32_t q6 = lq | hq;
+            const uint32_t e = __builtin_amdgcn_perm(0u, q6, 0x0c020c00u);   // bytes 0, 2 -> 16-bit lanes
+            const uint32_t o = __builtin_amdgcn_perm(0u, q6, 0x0c030c01u);   // bytes 1, 3
+            const uint32_t ve = __builtin_bit_cast(uint32_t, (s16x2)(__builtin_bit_cast(s16x2, e) * s2 + c2));
+            const uint32_t vo = __builtin_bit_cast(uint32_t, (s16x2)(__builtin_bit_cast(s16x2, o) * s2 + c2));
+            hh[i] = __builtin_amdgcn_perm(vo, ve, 0x07030501u);
+            ll[i] = __builtin_amdgcn_perm(vo, ve, 0x06020400u) ^ 0x80808080u;
+        }
+        hp[p] = v4i{(int)hh[0], (int)hh[1], (int)hh[2], (int)hh[3]};
+        lp[p] = v4i{(int)ll[0], (int)ll[1], (int)ll[2], (int)ll[3]};
+    }
+    v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[0]), hp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+    for (int p = 1; p < 4; p++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[p]), hp[p], acc, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[j] <<= 8;
+#pragma unroll
+    for (int p = 0; p < 4; p++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[p]), lp[p], acc, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = q6k_value(d, x.dx[j], acc[j]);
+}
+
+// ------------------------------------------------------------------ the kernel
+// Workgroup: 16 rows of one matrix, one wave per chunk of 4 super-blocks (ceil(G/4) <= 16 waves).
+template <int TYPE>
+__global__ void __launch_bounds__(1024)
+k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
+    constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    __shared__ float part[16][16][MV_ROWS];            // [chunk][token][row] chunk sums
+    const int lane = threadIdx.x & 63;
+    const int chunk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nchunks = blockDim.x >> 6;
+    const int q = lane >> 4, l16 = lane & 15;
+
+    const int wg = blockIdx.x;
+    const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
+    const int R = mg.R[m];
+    const int row0 = (wg - mg.first[m]) * MV_ROWS;
+    int row = row0 + l16;
+    row = row < R ? row : R - 1;                       // rows past R are loaded clamped, not stored
+    const int64_t col_bytes = 8 * BS;
+    const uint8_t* wrow = mg.w[m] + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
+    const int64_t xrow = (int64_t)G * Q8K_BYTES;
+    const uint8_t* xa = XQ + (int64_t)(l16 < N ? l16 : N - 1) * xrow;
+    const uint8_t* xd[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = 4 * q + j;
+        xd[j] = XQ + (int64_t)(n < N ? n : N - 1) * xrow;
+    }
+
+    // the chunk's four super-blocks; columns past G are loaded clamped and contribute +0
+    MvW<TYPE> w[2];
+    MvX x[2];
+    float v[MV_CHUNK][4];
+    auto load = [&](int s, MvW<TYPE>& ww, MvX& xx) {
+        int g = MV_CHUNK * chunk + s;
+        g = g < G ? g : G - 1;
+        mv_load(ww, wrow + (int64_t)g * col_bytes, q);
+        const uint8_t* xdg[4] = {xd[0] + g * Q8K_BYTES, xd[1] + g * Q8K_BYTES, xd[2] + g * Q8K_BYTES,
+                                 xd[3] + g * Q8K_BYTES};
+        mv_load_x(xx, xa + (int64_t)g * Q8K_BYTES, xdg, q);
+    };
+    load(0, w[0], x[0]);
+    load(1, w[1], x[1]);
+#pragma unroll
+    for (int s = 0; s < MV_CHUNK; s++) {
+        float vv[4];
+        mv_values(w[s & 1], x[s & 1], q, vv);
+        const bool valid = MV_CHUNK * chunk + s < G;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[s][j] = valid ? vv[j] : 0.0f;
+        if (s + 2 < MV_CHUNK) load(s + 2, w[s & 1], x[s & 1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        part[chunk][4 * q + j][l16] = __fadd_rn(__fadd_rn(v[0][j], v[1][j]), __fadd_rn(v[2][j], v[3][j]));
+    __syncthreads();
+
+    // merge: thread (token n, row r); passes of 4 chunks, missing chunks are +0
+    const int passes = (G + 15) / 16;
+    for (int idx = threadIdx.x; idx < N * MV_ROWS; idx += blockDim.x) {
+        const int n = idx / MV_ROWS, r = idx - n * MV_ROWS;
+        if (row0 + r >= R) continue;
+        PassTree tr;
+        tree_init(tr);
+        for (int ps = 0; ps < passes; ps++) {
+            float c[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int cc = 4 * ps + k;
+                c[k] = cc < nchunks ? part[cc][n][r] : 0.0f;
+            }
+            tree_push(tr, __fadd_rn(__fadd_rn(c[0], c[1]), __fadd_rn(c[2], c[3])));
+        }
+        mg.y[m][(int64_t)n * mg.ldy[m] + row0 + r] = tree_final(tr);
+    }
+}
+
+// n (1..3) matrices of one type, N = 1..16 tokens, C <= 16384 (at most 16 chunks of 4 columns).
+void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
+                            int N, float* const* y, const int64_t* ldy, hipStream_t s) {
+    const int G = C / QK;
+    MvGroup mg{};
+    int wgs = 0;
+    for (int i = 0; i < n; i++) {
+        mg.w[i] = w[i];
+        mg.y[i] = y[i];
+        mg.ldy[i] = ldy[i];
+        mg.R[i] = R[i];
+        mg.first[i] = wgs;
+        wgs += (R[i] + MV_ROWS - 1) / MV_ROWS;
+    }
+    for (int i = n; i < 4; i++) mg.first[i] = wgs;
+    const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
+    dim3 grid(wgs), block(64 * nchunks);
+    if (type == TYPE_Q4_K) hipLaunchKernelGGL(k_gemv_mfma<TYPE_Q4_K>, grid, block, 0, s, mg, xq, N, G);
+    else hipLaunchKernelGGL(k_gemv_mfma<TYPE_Q6_K>, grid, block, 0, s, mg, xq, N, G);
+}
+
+}  // namespace kq

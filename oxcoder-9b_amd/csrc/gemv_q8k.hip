@@ -23,11 +23,14 @@
 #ifndef KQ_GEMV_WAVES_PER_CU_Q6
 #define KQ_GEMV_WAVES_PER_CU_Q6 KQ_GEMV_WAVES_PER_CU
 #endif
+#ifndef KQ_GEMV_MFMA_MIN_N
+#define KQ_GEMV_MFMA_MIN_N 3     // tokens per call from which the MFMA form (gemv_mfma.hip) is used
+#endif
 #ifndef KQ_GEMV_SPLIT_MAX
 #define KQ_GEMV_SPLIT_MAX 4      // most column passes handled by the pass-split kernel (Q4_K)
 #endif
 #ifndef KQ_GEMV_SPLIT_MAX_Q6
-#define KQ_GEMV_SPLIT_MAX_Q6 2   // Q6_K: 3-4 passes run faster as sequential passes (measured)
+#define KQ_GEMV_SPLIT_MAX_Q6 2   // Q6_K, 1-2 tokens: 3-4 passes run faster as sequential passes (measured)
 #endif
 #ifndef KQ_GEMV_WG_WAVES
 #define KQ_GEMV_WG_WAVES 4
@@ -406,7 +409,9 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
     mg.first_unit[3] = total;
     const int passes = (G + 15) / 16;
     const int wpc = TYPE == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_Q6 : KQ_GEMV_WAVES_PER_CU;
-    if (passes <= (TYPE == TYPE_Q6_K ? KQ_GEMV_SPLIT_MAX_Q6 : KQ_GEMV_SPLIT_MAX)) {
+    // Q6_K with one or two tokens: sequential passes (the activations are reloaded per pass,
+    // which only pays off while they are few)
+    if (passes <= (TYPE == TYPE_Q6_K && NT <= 2 ? KQ_GEMV_SPLIT_MAX_Q6 : KQ_GEMV_SPLIT_MAX)) {
         // K unit streams of `passes` waves per workgroup (about KQ_GEMV_WG_WAVES waves per
         // workgroup); about KQ_GEMV_WAVES_PER_CU waves per CU in total
         const int K = passes >= KQ_GEMV_WG_WAVES ? 1 : KQ_GEMV_WG_WAVES / passes;
@@ -464,6 +469,10 @@ static void launch1(const MatGroup& mg, const uint8_t* xq, int G, int nt, int rp
 void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s) {
     const int G = C / QK;
+    if (N >= KQ_GEMV_MFMA_MIN_N && G <= 64) {   // 3..16 tokens: the MFMA form (same bits)
+        launch_gemv_mfma_group(n, w, R, C, type, xq, N, y, ldy, s);
+        return;
+    }
     for (int n0 = 0; n0 < N; n0 += 4) {
         const int nt = N - n0 < 4 ? N - n0 : 4;
         MatGroup mg{};

@@ -31,6 +31,9 @@ void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq
 // n (1..3) matrices of one type sharing xq; one launch per group of up to 4 tokens.
 void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s);
+// Small-batch GEMV on MFMA (C <= 16384, N <= 16): rows bit-identical to the GEMV above.
+void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
+                            int N, float* const* y, const int64_t* ldy, hipStream_t s);
 // Prefill GEMM; ws (or nullptr) holds gemm_q8k_workspace(C, M) bytes (16-byte aligned) for the
 // activation fragments.
 size_t gemm_q8k_workspace(int C, int M);

@@ -159,7 +159,10 @@ def test_gemv_q8k_reference_inputs(dev, orc, ty):
     assert_close_inf(host(y), orc.gemv_q8k(W, R, C, ty, xq, 1)[0])
 
 
-@pytest.mark.parametrize("ty,R,C", [(12, 12288, 4096), (14, 4096, 12288), (12, 64, 4352)])
+@pytest.mark.parametrize("ty,R,C", [
+    (12, 12288, 4096), (14, 4096, 12288), (12, 64, 4352),   # decode shapes; G = 17 (a padded pass)
+    (14, 8, 256), (12, 24, 16384), (14, 40, 16640),         # half row tile, one column; G = 64; G = 65
+])
 def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
     """Speculative-verify invariant: every row of a batch equals its N = 1 result bit for bit."""
     W = dev_t(synth(R, C, ty, 77), dev)
@@ -175,6 +178,23 @@ def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
         ops.gemv_q8k(W, R, C, ty, xqd[:N], N, yb, R + 8)
         np.testing.assert_array_equal(host(yb)[:, :R], s[:N])
     assert_close_inf(s, orc.gemv_q8k(host(W), R, C, ty, xq, 16))
+
+
+@pytest.mark.parametrize("ty", [12, 14])
+def test_batched_reference_inputs_bit_identical(dev, orc, ty):
+    """The reference unit test's random block bytes (any scale/min bit pattern) through the
+    batched path: rows equal the N = 1 results bit for bit and the oracle within the bar."""
+    W, x, R, C = reference_unit_inputs()[ty]
+    X = np.stack([x * (i + 1) * (-1) ** i for i in range(7)]).astype(np.float32)
+    xq = orc.quantize_q8k(X)
+    Wd, xqd = dev_t(W, dev), dev_t(xq, dev)
+    yb = torch.empty((7, R), device=dev)
+    ops.gemv_q8k(Wd, R, C, ty, xqd, 7, yb)
+    for n in range(7):
+        y1 = torch.empty(R, device=dev)
+        ops.gemv_q8k(Wd, R, C, ty, xqd[n:n + 1], 1, y1)
+        np.testing.assert_array_equal(host(yb)[n], host(y1))
+    assert_close_inf(host(yb), orc.gemv_q8k(W, R, C, ty, xq, 7))
 
 
 @pytest.mark.parametrize("N", [1, 3, 6])

@@ -271,8 +271,8 @@ def gemm_extra(torch, rn, dev, timed=True):
                 torch.cuda.synchronize()
                 continue
             g = capture(torch, lambda: rn.gemm(w, R, C_, ty, xq, M, y, ws, rn.stream()))
-            time_graphs(torch, [g])
-            reps = 3
+            time_graphs(torch, [g] * 10)   # warm-up: clocks settle under sustained MFMA load
+            reps = 10
             el = time_graphs(torch, [g] * reps) / reps
             out["%s_M%d" % (name, M)] = {"us": round(el * 1e6, 1), "TOPS": round(2 * M * R * C_ / el / 1e12, 2),
                                          "frac_int8_peak": round(2 * M * R * C_ / el / 1e12 / INT8_PEAK_TOPS, 4)}

@@ -97,7 +97,7 @@ size_t kq_gemm_q8k_workspace(int C, int M);
 
 /*
  * kq_gemm_q8k with a caller-provided workspace (ws 256-byte aligned, ws_bytes at least
- * kq_gemm_q8k_workspace(C, M), about M*C bytes with M rounded up to 128).  The call first copies
+ * kq_gemm_q8k_workspace(C, M), about M*C bytes with M rounded up to 256).  The call first copies
  * the activation quants into ws in MFMA fragment order, so that every operand load of the GEMM is
  * one contiguous 1 KB.  Allocates nothing; calls sharing a workspace must be ordered (same stream
  * or synchronised).

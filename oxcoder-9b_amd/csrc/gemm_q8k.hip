@@ -33,6 +33,8 @@
 // the fragments are read from the Q8_K rows directly.  The next super-block's raw weight bytes
 // and activation fragments are loaded one step ahead.  Rows past M or R are clamped for loading
 // and not stored.
+#include <type_traits>
+
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -46,7 +48,29 @@ typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int GM_BM = 128;   // tokens per workgroup
+constexpr int GM_BMAX = 256;  // largest token tile: the fragment workspace is padded to it
+
+#ifndef KQ_GEMM_WN128
+#define KQ_GEMM_WN128 2   // waves along n for 128-row tiles
+#endif
+#ifndef KQ_GEMM_BM256
+#define KQ_GEMM_BM256 0   // 256-token tiles (8 waves, two per SIMD); spills at 256 VGPRs, off
+#endif
+#ifndef KQ_GEMM_IGLP
+// Instruction scheduling of the main loop (all forms give the same bits):
+//   0: compiler order; 1: lo sweep in two tile groups, the first group's epilogue after the second
+//   group's MFMAs; 2: 1 + MFMA/VALU interleave hints in both sweeps; 3: 2 with the hi sweep left to
+//   iglp_opt(1); 4: 1 + the unpack of the next super-block woven between the hi-sweep K steps.
+// Measured (us, Q4_K 12288x4096 / Q6_K 4096x12288 at M = 512, 2048): 0: 98/411/128/397,
+// 1: 92/367/120/397, 2: 85/361/104/377, 3: 79-87/343/96/369, 4: 94/331/116/379.
+#define KQ_GEMM_IGLP 3
+#endif
+#ifndef KQ_GEMM_VPM
+#define KQ_GEMM_VPM 5     // VALU instructions scheduled per MFMA in the hi sweep (unpack of the next super-block)
+#endif
+#ifndef KQ_GEMM_VPM2
+#define KQ_GEMM_VPM2 7    // VALU instructions per MFMA in the second lo-sweep group (first group's epilogue)
+#endif
 
 // Byte offset of 16-byte chunk `c` (0..15) of LDS plane row `r`: rows are 256 B, the chunk index
 // is XORed with the row's low 4 bits.
@@ -63,12 +87,14 @@ __device__ __forceinline__ void st16(int8_t* p, uint32_t a, uint32_t b, uint32_t
     *reinterpret_cast<u32x4*>(p) = u32x4{a, b, c, d};
 }
 
-template <int BN> struct GemmLds {
-    int8_t wh[2][BN * 256];
-    int8_t wl[2][BN * 256];
-    uint32_t wmin[2][BN * 8];      // Q4_K: row n = 16 f16 [-64 m_0..7, -m_0..7]
-    uint32_t xmin[2][GM_BM * 8];   // Q4_K: row m = 16 f16 [B_0..7 >> 6, B_0..7 & 63]
-    float d[2][BN], dm[2][BN], dx[2][GM_BM];
+// One LDS buffer (the kernel double-buffers with two of them: distinct objects, so the compiler
+// knows the next super-block's stores never alias the current one's loads).
+template <int BN, int BM> struct GemmBuf {
+    int8_t wh[BN * 256];
+    int8_t wl[BN * 256];
+    uint32_t wmin[BN * 8];      // Q4_K: row n = 16 f16 [-64 m_0..7, -m_0..7]
+    uint32_t xmin[BM * 8];      // Q4_K: row m = 16 f16 [B_0..7 >> 6, B_0..7 & 63]
+    float d[BN], dm[BN], dx[BM];
 };
 
 // ------------------------------------------------------------------ weight parts
@@ -124,20 +150,26 @@ __device__ __forceinline__ void load_raw(RawW<TYPE_Q6_K, PPR>& r, const uint8_t*
     r.dw = ld4(b4 + 208);
 }
 
-// Unpack into LDS buffer `L.*[buf]`, weight row `row` (0..BN-1).
-template <int PPR, int BN>
-__device__ __forceinline__ void unpack(const RawW<TYPE_Q4_K, PPR>& r, int pi, int row, GemmLds<BN>& L, int buf) {
+// Unpack into LDS buffer Lb, weight row `row` (0..BN-1).  The work comes in UNPACK_PIECES pieces;
+// `only` selects one of them (-1: all), so the kernel can spread the unpack between MFMAs.
+constexpr int UNPACK_PIECES = 4;
+template <int PPR, int BN, int BM>
+__device__ __forceinline__ void unpack(const RawW<TYPE_Q4_K, PPR>& r, int pi, int row, GemmBuf<BN, BM>& Lb,
+                                       int only = -1) {
     constexpr int NPP = RawW<TYPE_Q4_K, PPR>::NPP;
-    int8_t* wh = L.wh[buf];
-    int8_t* wl = L.wl[buf];
+    constexpr int PER = 2 * NPP / UNPACK_PIECES > 0 ? 2 * NPP / UNPACK_PIECES : 1;   // (pp, c) steps per piece
+    int8_t* wh = Lb.wh;
+    int8_t* wl = Lb.wl;
 #pragma unroll
     for (int pp = 0; pp < NPP; pp++) {
+        if (only >= 0 && only != (2 * pp) / PER && only != (2 * pp + 1) / PER) continue;
         const int p = pi * NPP + pp;
         const ScMin sm = q4k_scmin_pair(r.hdr.y, r.hdr.z, r.hdr.w, p);
         const uint32_t alo = (sm.sc_lo >> 3) * 0x10001u, blo = (sm.sc_lo & 7u) * 0x10001u;
         const uint32_t ahi = (sm.sc_hi >> 3) * 0x10001u, bhi = (sm.sc_hi & 7u) * 0x10001u;
 #pragma unroll
         for (int c = 0; c < 2; c++) {          // elements 64p + 16c + 0..15 (lo), 64p + 32 + 16c (hi)
+            if (only >= 0 && only != (2 * pp + c) / PER) continue;
             const u32x4 v = r.q[2 * pp + c];
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
             uint32_t h0[4], l0[4], h1[4], l1[4];
@@ -155,26 +187,33 @@ __device__ __forceinline__ void unpack(const RawW<TYPE_Q4_K, PPR>& r, int pi, in
             st16(wh + swz(row, c1), h1[0], h1[1], h1[2], h1[3]);
             st16(wl + swz(row, c1), l1[0], l1[1], l1[2], l1[3]);
         }
-        const float mlo = (float)sm.m_lo, mhi = (float)sm.m_hi;
-        L.wmin[buf][row * 8 + p] = pk_f16(-64.0f * mlo, -64.0f * mhi);
-        L.wmin[buf][row * 8 + 4 + p] = pk_f16(-mlo, -mhi);
+        if (only < 0 || only == (2 * pp + 1) / PER) {
+            const float mlo = (float)sm.m_lo, mhi = (float)sm.m_hi;
+            Lb.wmin[row * 8 + p] = pk_f16(-64.0f * mlo, -64.0f * mhi);
+            Lb.wmin[row * 8 + 4 + p] = pk_f16(-mlo, -mhi);
+        }
     }
     // every part of the row stores the same d / dmin: no branch in the main loop
-    L.d[buf][row] = f16_lo(r.hdr.x);
-    L.dm[buf][row] = f16_hi(r.hdr.x);
+    if (only < 0 || only == UNPACK_PIECES - 1) {
+        Lb.d[row] = f16_lo(r.hdr.x);
+        Lb.dm[row] = f16_hi(r.hdr.x);
+    }
 }
 
-template <int PPR, int BN>
-__device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, int row, GemmLds<BN>& L, int buf) {
+template <int PPR, int BN, int BM>
+__device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, int row, GemmBuf<BN, BM>& Lb,
+                                       int only = -1) {
     constexpr int NJ = RawW<TYPE_Q6_K, PPR>::NJ;
+    constexpr int PER = 4 * NJ / UNPACK_PIECES;                  // (j, k) steps per piece
     const int h = NJ == 2 ? pi : pi >> 1, jj0 = NJ == 2 ? 0 : pi & 1;
-    int8_t* wh = L.wh[buf];
-    int8_t* wl = L.wl[buf];
+    int8_t* wh = Lb.wh;
+    int8_t* wl = Lb.wl;
     const uint32_t sh = r.sh;
     const uint32_t s0 = __builtin_amdgcn_alignbyte(r.sc.y, r.sc.x, sh);   // scales 8h .. 8h+3
     const uint32_t s1 = __builtin_amdgcn_alignbyte(r.sce, r.sc.y, sh);    // scales 8h+4 .. 8h+7
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
+        if (only >= 0 && only / (4 / PER) != j) continue;
         const int jj = jj0 + j;
         uint32_t Lw[2][4], Hw[4];
 #pragma unroll
@@ -194,6 +233,7 @@ __device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, in
         }
 #pragma unroll
         for (int k = 0; k < 4; k++) {              // elements 128h + 32k + 16jj + 0..15
+            if (only >= 0 && only != (4 * j + k) / PER) continue;
             const uint32_t scw = k < 2 ? s0 : s1;
             const int sc = (int)(int8_t)(uint8_t)(scw >> (8 * ((2 * k + jj) & 3)));
             const uint32_t s2 = (uint32_t)(sc & 0xffff) * 0x10001u;
@@ -217,7 +257,8 @@ __device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, in
             st16(wl + swz(row, ch), lb[0], lb[1], lb[2], lb[3]);
         }
     }
-    L.d[buf][row] = f16_lo(r.dw >> (8 * sh));   // same value from every part of the row
+    if (only < 0 || only == UNPACK_PIECES - 1)
+        Lb.d[row] = f16_lo(r.dw >> (8 * sh));   // same value from every part of the row
 }
 
 // ------------------------------------------------------------------ activation side
@@ -241,8 +282,8 @@ __device__ __forceinline__ void load_x(RawX<XP>& r, const uint8_t* xb, int xp) {
     r.d = ld4(xb);
 }
 
-template <int TYPE, int XP, int BN>
-__device__ __forceinline__ void stage_x(const RawX<XP>& r, int mr, int xp, GemmLds<BN>& L, int buf) {
+template <int TYPE, int XP, int BN, int BM>
+__device__ __forceinline__ void stage_x(const RawX<XP>& r, int mr, int xp, GemmBuf<BN, BM>& Lb) {
     constexpr int NB = RawX<XP>::NB;
     if (TYPE == TYPE_Q4_K) {
         // B_s = bsum[2s] + bsum[2s+1] for s = NB*xp .. NB*xp+NB-1, split as 64 * (B >> 6) + (B & 63)
@@ -252,35 +293,38 @@ __device__ __forceinline__ void stage_x(const RawX<XP>& r, int mr, int xp, GemmL
 #pragma unroll
         for (int i = 0; i < NB; i += 2) {
             const int dw = mr * 8 + (NB * xp + i) / 2;
-            L.xmin[buf][dw] = pk_f16((float)(B[i] >> 6), (float)(B[i + 1] >> 6));
-            L.xmin[buf][dw + 4] = pk_f16((float)(B[i] & 63), (float)(B[i + 1] & 63));
+            Lb.xmin[dw] = pk_f16((float)(B[i] >> 6), (float)(B[i + 1] >> 6));
+            Lb.xmin[dw + 4] = pk_f16((float)(B[i] & 63), (float)(B[i + 1] & 63));
         }
     }
-    L.dx[buf][mr] = __builtin_bit_cast(float, r.d);   // same value from every part of the row
+    Lb.dx[mr] = __builtin_bit_cast(float, r.d);   // same value from every part of the row
 }
 
 // ------------------------------------------------------------------ the kernel
-// WN waves along n (2 or 4) times 2 along m; each wave owns 64 tokens x BN/WN weight rows.
-// FRAG: A operands from the fragment-order copy XF, else straight from the Q8_K rows XQ.
-template <int TYPE, int BN, int WN, bool FRAG>
-__global__ void __launch_bounds__(128 * WN)
+// WN waves along n (2 or 4) times WM (2 or 4) along m; each wave owns 64 tokens x BN/WN weight
+// rows, the workgroup BM = 64*WM tokens.  FRAG: A operands from the fragment-order copy XF, else
+// straight from the Q8_K rows XQ.
+template <int TYPE, int BN, int WN, int WM, bool FRAG>
+__global__ void __launch_bounds__(64 * WN * WM)
 k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restrict__ XQ,
            const uint8_t* __restrict__ XF, int M, float* __restrict__ Y, int64_t ldy) {
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
-    constexpr int NTHR = 128 * WN;
+    constexpr int BM = 64 * WM;
+    constexpr int NTHR = 64 * WN * WM;
     constexpr int NE = BN / WN;                   // weight rows per wave
     constexpr int NT = NE / 32;                   // 32-column MFMA tiles per wave
     constexpr int PPR = NTHR / BN;                // unpack parts per weight row
-    constexpr int XP = NTHR / GM_BM;              // staging parts per activation row
+    constexpr int XP = NTHR / BM;                 // staging parts per activation row
     constexpr int SHIFT = TYPE == TYPE_Q4_K ? 3 : 8;
     static_assert(PPR == 2 || PPR == 4, "a weight row is split in 2 or 4 parts");
     static_assert(NT >= 1, "at least one 32-row tile per wave");
-    __shared__ __attribute__((aligned(16))) GemmLds<BN> L;
+    __shared__ __attribute__((aligned(16))) GemmBuf<BN, BM> LB0;
+    __shared__ __attribute__((aligned(16))) GemmBuf<BN, BM> LB1;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % WM, wn = wave / WM;
     const int half = lane >> 5, l32 = lane & 31;
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * GM_BM;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
 
     // A operand of this lane for K step ks of super-block g: afrag[mt] + g * AG + ks * AK
@@ -289,7 +333,7 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
 #pragma unroll
     for (int mt = 0; mt < 2; mt++) {
         if (FRAG) {   // fragment tile (m0 + 64 wm + 32 mt) / 32
-            afrag[mt] = XF + ((int64_t)(blockIdx.y * 4 + 2 * wm + mt) * G * 512 + lane) * 16;
+            afrag[mt] = XF + ((int64_t)(blockIdx.y * (BM / 32) + 2 * wm + mt) * G * 512 + lane) * 16;
         } else {      // row m, bytes 32 ks + 16 half of its quants
             int m = m0 + 64 * wm + 32 * mt + l32;
             m = m < M ? m : M - 1;
@@ -297,7 +341,7 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
         }
     }
     // activation row staged by this thread
-    const int mr = tid & 127, xp = tid >> 7;
+    const int mr = tid % BM, xp = tid / BM;
     const uint8_t* xstage = XQ + (int64_t)(m0 + mr < M ? m0 + mr : M - 1) * xrow;
     // weight row part unpacked by this thread
     const int prow = tid % BN, pi = tid / BN;
@@ -322,8 +366,8 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + ks * AK));
-    unpack(raw, pi, prow, L, 0);
-    stage_x<TYPE>(rx, mr, xp, L, 0);
+    unpack(raw, pi, prow, LB0);
+    stage_x<TYPE>(rx, mr, xp, LB0);
     {
         const int g1 = G > 1 ? 1 : 0;
         load_raw(raw, wrow + (int64_t)g1 * 8 * BS, pi);
@@ -332,28 +376,53 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     __syncthreads();
 
     const int nrow0 = wn * NE + l32;        // this lane's B rows: nrow0 + 32 nt
-    for (int g = 0; g < G; g++) {
-        const int cur = g & 1, nxt = cur ^ 1;
+    // One super-block step; the LDS buffer index is a compile-time constant (the loop is unrolled
+    // by two) so the compiler can tell the next buffer's stores from the current buffer's loads and
+    // overlap the unpack with the MFMAs.
+    auto step = [&](auto cur_c, int g) {
+        constexpr int cur = decltype(cur_c)::value;
+        GemmBuf<BN, BM>& Lc = cur ? LB1 : LB0;   // read this step
+        GemmBuf<BN, BM>& Ln = cur ? LB0 : LB1;   // filled for the next step
 
+        const int g2 = g + 2 < G ? g + 2 : G - 1;
+        v16i acc[2][NT];
+#if KQ_GEMM_IGLP >= 4
+        // ---- hi sweep, with the unpack of super-block g+1 into the other buffer woven in: one
+        //      piece after every second K step, each step fenced off so the MFMAs of a K step run
+        //      while the next piece's VALU work issues; then fetch the raw bytes of g+2
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            v4i b[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) b[nt] = *reinterpret_cast<const v4i*>(Lc.wh + swz(nrow0 + 32 * nt, 2 * ks + half));
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt],
+                                                                        ks == 0 ? v16i{} : acc[mt][nt], 0, 0, 0);
+            if (ks & 1) unpack(raw, pi, prow, Ln, ks >> 1);
+            if (ks == 6) stage_x<TYPE>(rx, mr, xp, Ln);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        load_raw(raw, wrow + (int64_t)g2 * 8 * BS, pi);
+        load_x(rx, xstage + (int64_t)g2 * Q8K_BYTES, xp);
+#else
         // ---- stage super-block g+1 into the other buffer (last iteration: a harmless repeat),
         //      then fetch the raw bytes of g+2
-        unpack(raw, pi, prow, L, nxt);
-        stage_x<TYPE>(rx, mr, xp, L, nxt);
-        {
-            const int g2 = g + 2 < G ? g + 2 : G - 1;
-            load_raw(raw, wrow + (int64_t)g2 * 8 * BS, pi);
-            load_x(rx, xstage + (int64_t)g2 * Q8K_BYTES, xp);
-        }
+        unpack(raw, pi, prow, Ln);
+        stage_x<TYPE>(rx, mr, xp, Ln);
+        load_raw(raw, wrow + (int64_t)g2 * 8 * BS, pi);
+        load_x(rx, xstage + (int64_t)g2 * Q8K_BYTES, xp);
 
         // ---- main sweeps: I = 2^SHIFT * (A . H) + (A . L)
-        v16i acc[2][NT];
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
             v4i b[NT];
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const int r = nrow0 + 32 * nt;
-                b[nt] = *reinterpret_cast<const v4i*>(L.wh[cur] + swz(r, 2 * ks + half));
+                b[nt] = *reinterpret_cast<const v4i*>(Lc.wh + swz(r, 2 * ks + half));
             }
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
@@ -362,20 +431,135 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
                     acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt],
                                                                         ks == 0 ? v16i{} : acc[mt][nt], 0, 0, 0);
         }
+#endif
+#if KQ_GEMM_IGLP >= 2 && KQ_GEMM_IGLP < 4
+        // hi sweep: one MFMA, then a share of the unpack of super-block g+1 (VALU, LDS stores)
+#if KQ_GEMM_IGLP == 3
+        __builtin_amdgcn_iglp_opt(1);
+#else
+#pragma unroll
+        for (int i = 0; i < 8 * NT; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read (B operand)
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, KQ_GEMM_VPM, 0);   // VALU (unpack)
+            __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);   // DS write (unpack)
+        }
+#endif
+        __builtin_amdgcn_sched_barrier(0);
+#endif
+        const int gn = g + 1 < G ? g + 1 : G - 1;
+
+        // epilogue of one 32x32 tile of super-block g
+        auto epilogue = [&](int mt, int nt) {
+            f32x4 dxv[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                dxv[q] = *reinterpret_cast<const f32x4*>(&Lc.dx[64 * wm + 32 * mt + 8 * q + 4 * half]);
+            const int ml = 64 * wm + 32 * mt + l32;
+            const int nl = nrow0 + 32 * nt;
+            const float dn = Lc.d[nl];
+            if (TYPE == TYPE_Q4_K) {
+                const float dmn = Lc.dm[nl];
+                const v8h bm = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&Lc.wmin[nl * 8 + 4 * half]));
+                const v8h am = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&Lc.xmin[ml * 8 + 4 * half]));
+                const v16f cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, v16f{}, 0, 0, 0);   // -I2
+#pragma unroll
+                for (int a = 0; a < 16; a++) {
+                    const float t = __builtin_fmaf(dmn, cm[a], __fmul_rn(dn, (float)acc[mt][nt][a]));
+                    yacc[mt][nt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], t, yacc[mt][nt][a]);
+                }
+            } else {
+#pragma unroll
+                for (int a = 0; a < 16; a++)
+                    yacc[mt][nt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], __fmul_rn(dn, (float)acc[mt][nt][a]),
+                                                     yacc[mt][nt][a]);
+            }
+        };
+        auto shift = [&](int mt, int nt) {
+#pragma unroll
+            for (int a = 0; a < 16; a++) acc[mt][nt][a] <<= SHIFT;
+        };
+#if KQ_GEMM_IGLP >= 1
+        // lo sweep in two tile groups (NT = 2: by nt, NT = 1: by mt); the epilogue of the first
+        // group runs under the MFMAs of the second
+        if constexpr (NT == 2) {
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) shift(mt, 0);
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                const v4i b = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0, 2 * ks + half));
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+                    acc[mt][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b, acc[mt][0], 0, 0, 0);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) shift(mt, 1);
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                const v4i b = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0 + 32, 2 * ks + half));
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+                    acc[mt][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b, acc[mt][1], 0, 0, 0);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) epilogue(mt, 0);
+#if KQ_GEMM_IGLP >= 2
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, KQ_GEMM_VPM2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#endif
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+                    afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) epilogue(mt, 1);
+        } else {
+            v4i b[8];
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) b[ks] = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0, 2 * ks + half));
+            shift(0, 0);
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+                acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[0][ks], b[ks], acc[0][0], 0, 0, 0);
+            shift(1, 0);
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+                acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[1][ks], b[ks], acc[1][0], 0, 0, 0);
+            epilogue(0, 0);
+#if KQ_GEMM_IGLP >= 2
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, KQ_GEMM_VPM2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#endif
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+                    afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
+            epilogue(1, 0);
+        }
+#else
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-                for (int a = 0; a < 16; a++) acc[mt][nt][a] <<= SHIFT;
-        const int gn = g + 1 < G ? g + 1 : G - 1;
+            for (int nt = 0; nt < NT; nt++) shift(mt, nt);
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
             v4i b[NT];
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const int r = nrow0 + 32 * nt;
-                b[nt] = *reinterpret_cast<const v4i*>(L.wl[cur] + swz(r, 2 * ks + half));
+                b[nt] = *reinterpret_cast<const v4i*>(Lc.wl + swz(r, 2 * ks + half));
             }
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
@@ -387,38 +571,16 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
             for (int mt = 0; mt < 2; mt++)
                 afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
         }
-
-        // ---- epilogue of super-block g
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-            f32x4 dxv[4];
+        for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-                dxv[q] = *reinterpret_cast<const f32x4*>(&L.dx[cur][64 * wm + 32 * mt + 8 * q + 4 * half]);
-            const int ml = 64 * wm + 32 * mt + l32;
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const int nl = nrow0 + 32 * nt;
-                const float dn = L.d[cur][nl];
-                if (TYPE == TYPE_Q4_K) {
-                    const float dmn = L.dm[cur][nl];
-                    const v8h bm = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&L.wmin[cur][nl * 8 + 4 * half]));
-                    const v8h am = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&L.xmin[cur][ml * 8 + 4 * half]));
-                    const v16f cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, v16f{}, 0, 0, 0);   // -I2
-#pragma unroll
-                    for (int a = 0; a < 16; a++) {
-                        const float t = __builtin_fmaf(dmn, cm[a], __fmul_rn(dn, (float)acc[mt][nt][a]));
-                        yacc[mt][nt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], t, yacc[mt][nt][a]);
-                    }
-                } else {
-#pragma unroll
-                    for (int a = 0; a < 16; a++)
-                        yacc[mt][nt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], __fmul_rn(dn, (float)acc[mt][nt][a]),
-                                                         yacc[mt][nt][a]);
-                }
-            }
-        }
+            for (int nt = 0; nt < NT; nt++) epilogue(mt, nt);
+#endif
         __syncthreads();
+    };
+    for (int g = 0; g < G; g += 2) {
+        step(std::integral_constant<int, 0>{}, g);
+        if (g + 1 < G) step(std::integral_constant<int, 1>{}, g + 1);
     }
 
     // ---- store
@@ -435,11 +597,8 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     }
 }
 
-#ifndef KQ_GEMM_WN128
-#define KQ_GEMM_WN128 2   // waves along n for 128-row tiles
-#endif
 
-// Fragment-order copy of the activation quants (layout above); rows M .. 128*ceil(M/128)-1 are
+// Fragment-order copy of the activation quants (layout above); rows M .. 256*ceil(M/256)-1 are
 // zero.  One workgroup per (32-row tile, super-block), 32 bytes per thread.
 __global__ void __launch_bounds__(256)
 k_q8k_frag(const uint8_t* __restrict__ XQ, int M, int G, uint8_t* __restrict__ XF) {
@@ -457,31 +616,41 @@ k_q8k_frag(const uint8_t* __restrict__ XQ, int M, int G, uint8_t* __restrict__ X
 }
 
 size_t gemm_q8k_workspace(int C, int M) {
-    return (size_t)((M + GM_BM - 1) / GM_BM) * GM_BM * (size_t)C;
+    return (size_t)((M + GM_BMAX - 1) / GM_BMAX) * GM_BMAX * (size_t)C;
 }
 
-template <int TYPE, int BN, int WN>
+template <int TYPE, int BN, int WN, int WM>
 static void launch_tile(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
                         int64_t ldy, hipStream_t s) {
-    dim3 grid((R + BN - 1) / BN, (M + GM_BM - 1) / GM_BM), block(128 * WN);
-    if (xf) hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, true>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
-    else hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, false>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
+    constexpr int BM = 64 * WM;
+    dim3 grid((R + BN - 1) / BN, (M + BM - 1) / BM), block(64 * WN * WM);
+    if (xf) hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
+    else hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
 }
 
 template <int TYPE>
 static void launch_type(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
                         int64_t ldy, hipStream_t s) {
-    // 128-row tiles when they give at least two workgroups per CU in total, else 64-row tiles
-    const int64_t tiles128 = (int64_t)((R + 127) / 128) * ((M + GM_BM - 1) / GM_BM);
-    if (tiles128 >= 2 * (int64_t)device_cus()) launch_tile<TYPE, 128, KQ_GEMM_WN128>(w, R, G, xq, xf, M, y, ldy, s);
-    else launch_tile<TYPE, 64, 2>(w, R, G, xq, xf, M, y, ldy, s);
+    // the largest tile that still gives at least two workgroups per CU in total
+    const int64_t cus = device_cus();
+    const int64_t t256 = (int64_t)((R + 127) / 128) * ((M + 255) / 256);
+    const int64_t t128 = (int64_t)((R + 127) / 128) * ((M + 127) / 128);
+    if constexpr (KQ_GEMM_BM256) {
+        if (t256 >= 2 * cus) {
+            launch_tile<TYPE, 128, 2, 4>(w, R, G, xq, xf, M, y, ldy, s);
+            return;
+        }
+    }
+    (void)t256;
+    if (t128 >= 2 * cus) launch_tile<TYPE, 128, KQ_GEMM_WN128, 2>(w, R, G, xq, xf, M, y, ldy, s);
+    else launch_tile<TYPE, 64, 2, 2>(w, R, G, xq, xf, M, y, ldy, s);
 }
 
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
                      uint8_t* ws, hipStream_t s) {
     const int G = C / QK;
     if (ws) {
-        dim3 fgrid((M + GM_BM - 1) / GM_BM * (GM_BM / 32), G);
+        dim3 fgrid((M + GM_BMAX - 1) / GM_BMAX * (GM_BMAX / 32), G);
         hipLaunchKernelGGL(k_q8k_frag, fgrid, dim3(256), 0, s, xq, M, G, ws);
     }
     if (type == TYPE_Q4_K) launch_type<TYPE_Q4_K>(w, R, G, xq, ws, M, y, ldy, s);

@@ -57,9 +57,11 @@ template <int TYPE> struct Frag;
 template <> struct Frag<TYPE_Q4_K> { u32x4 hdr, qa, qb; };
 // Q6_K fields sit at block offset + (block start & 3): a lane multiplies its dword-aligned words
 // (each 16-B field + the following dword), the scales and d, funnel-shifted by the byte shift in
-// block_value.
+// block_value.  A lane loads its three 16-B quant fields and the quad's common 16-B scale field
+// and d dword (5 loads); the dword after each quant field is the first dword of a field another
+// lane of the quad holds, and comes from it by a quad permutation (prepare).
 struct Q6Fields { u32x4 l0, l1, hb; uint32_t l0e, l1e, hbe; u32x2 sc; uint32_t sce, dw, sh; };
-template <> struct Frag<TYPE_Q6_K> { Q6Fields f; };
+template <> struct Frag<TYPE_Q6_K> { u32x4 l0, l1, hb, sc4; uint32_t dw, sh; };
 
 template <int TYPE> struct Act;
 template <> struct Act<TYPE_Q4_K> { uint32_t xl[8], xh[8]; int blo, bhi; float dx; };
@@ -75,25 +77,37 @@ __device__ __forceinline__ void load_frag(Frag<TYPE_Q4_K>& f, const uint8_t* bk,
 // the scale window [192 + 8h, 200 + 8h) and d [208, 210) are read from the dword-aligned address
 // at or below them; for even rows (block start = 0 mod 4) the last word read reaches 2 bytes
 // into the next row's block, which exists because row 7 of a tile is odd.
-__device__ __forceinline__ void load_frag(Frag<TYPE_Q6_K>& fr, const uint8_t* bk, int p) {
-    Q6Fields& f = fr.f;
+__device__ __forceinline__ void load_frag(Frag<TYPE_Q6_K>& f, const uint8_t* bk, int p) {
     const int h = p >> 1, jj = p & 1;
     // pointer arithmetic (not an integer round trip) keeps the global address space
     f.sh = uint32_t(reinterpret_cast<uintptr_t>(bk) & 3);   // the same shift for every field
     const uint8_t* b4 = bk - f.sh;
-    f.l0 = ld16_a4(b4 + h * 64 + 16 * jj);
-    f.l0e = ld4(b4 + h * 64 + 16 * jj + 16);
-    f.l1 = ld16_a4(b4 + h * 64 + 32 + 16 * jj);
-    f.l1e = ld4(b4 + h * 64 + 32 + 16 * jj + 16);
-    f.hb = ld16_a4(b4 + 128 + h * 32 + 16 * jj);
-    f.hbe = ld4(b4 + 128 + h * 32 + 16 * jj + 16);
-    f.sc = *reinterpret_cast<const u32x2_a4*>(b4 + 192 + 8 * h);
-    f.sce = ld4(b4 + 200 + 8 * h);
-    f.dw = ld4(b4 + 208);
+    f.l0 = ld16_a4(b4 + h * 64 + 16 * jj);          // ql bytes 64h + 16jj ..
+    f.l1 = ld16_a4(b4 + h * 64 + 32 + 16 * jj);     // ql bytes 64h + 32 + 16jj ..
+    f.hb = ld16_a4(b4 + 128 + h * 32 + 16 * jj);    // qh bytes 32h + 16jj ..
+    f.sc4 = ld16_a4(b4 + 192);                      // the 16 scales
+    f.dw = ld4(b4 + 208);                           // d
 }
-// The fields a lane multiplies (the fragment itself for both types).
-__device__ __forceinline__ const Q6Fields& prepare(const Frag<TYPE_Q6_K>& f) { return f.f; }
-__device__ __forceinline__ const Frag<TYPE_Q4_K>& prepare(const Frag<TYPE_Q4_K>& f) { return f; }
+// The fields a lane multiplies.  Quad lane p = 2h + jj holds the 16-B chunks at block offsets
+// (relative to the dword-aligned start) l0: 64h + 16jj, l1: 64h + 32 + 16jj, hb: 128 + 32h + 16jj,
+// so the dword following
+//   l0 of p = 0, 1, 2, 3 (offsets 16, 32, 80, 96) is l0.x of lane 1, l1.x of lane 0, l0.x of lane 3, l1.x of lane 2;
+//   l1 (offsets 48, 64, 112, 128) is l1.x of lane 1, l0.x of lane 2, l1.x of lane 3, hb.x of lane 0;
+//   hb (offsets 144, 160, 176, 192) is hb.x of lanes 1, 2, 3 and, for p = 3, the first scale dword.
+__device__ __forceinline__ Q6Fields prepare(const Frag<TYPE_Q6_K>& f, int p) {
+    constexpr int QUAD_ROT1 = 0x39;   // quad_perm [1,2,3,0]: lane i <- lane (i + 1) & 3
+    const int h = p >> 1, jj = p & 1;
+    Q6Fields q;
+    q.l0 = f.l0; q.l1 = f.l1; q.hb = f.hb; q.dw = f.dw; q.sh = f.sh;
+    q.l0e = (uint32_t)dpp<DPP_QUAD_XOR1>((int)(jj ? f.l0.x : f.l1.x));
+    q.l1e = (uint32_t)dpp<QUAD_ROT1>((int)(p == 0 ? f.hb.x : (p == 2 ? f.l0.x : f.l1.x)));
+    const uint32_t hn = (uint32_t)dpp<QUAD_ROT1>((int)f.hb.x);
+    q.hbe = p == 3 ? f.sc4.x : hn;
+    q.sc = h ? u32x2{f.sc4.z, f.sc4.w} : u32x2{f.sc4.x, f.sc4.y};   // scales 8h .. 8h+7
+    q.sce = h ? f.dw : f.sc4.z;                                     // the dword after them
+    return q;
+}
+__device__ __forceinline__ const Frag<TYPE_Q4_K>& prepare(const Frag<TYPE_Q4_K>& f, int) { return f; }
 __device__ __forceinline__ u32x4 funnel(const u32x4& v, uint32_t e, uint32_t sh) {
     u32x4 r;
     r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
@@ -232,7 +246,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
         }
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const auto& fr = prepare(cur[r]);
+            const auto fr = prepare(cur[r], p);
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 const float v = block_value(fr, act[t], p);
@@ -335,7 +349,7 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < RPW; r++) {
-                const auto& fr = prepare(cur[r]);
+                const auto fr = prepare(cur[r], p);
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     const float v = block_value(fr, act[t], p);
@@ -383,17 +397,16 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
 }
 
 // ------------------------------------------------------------------ launch
-// Rows per wave: 2 keeps per-wave register use moderate and gives many units to balance;
-// with several tokens per launch the register budget is NT*RPW <= 8 outputs per lane.
+// Rows per wave: Q4_K 2 keeps per-wave register use moderate and gives many units to balance;
+// with several tokens per launch the register budget is NT*RPW <= 8 outputs per lane.  Q6_K
+// takes one row per wave: twice the units, so each wave walks more (unit, pass) steps and its
+// prefetch covers more of the stream (4096x12288 at one token: 12.3 us against 14.2 us at 2).
 static int pick_rpw(int nt, int type) {
-#ifdef KQ_GEMV_RPW_Q6
-    if (type == TYPE_Q6_K) return KQ_GEMV_RPW_Q6;
-#endif
-    (void)type;
 #ifdef KQ_GEMV_RPW
-    (void)nt;
+    (void)nt; (void)type;
     return KQ_GEMV_RPW;
 #else
+    if (type == TYPE_Q6_K) return 1;
     return nt >= 3 ? 1 : 2;
 #endif
 }

@@ -18,17 +18,19 @@
 //   Q4_K: dx * (d * I1 - dmin * I2)          Q6_K: dx * (d * I)
 // (the per-super-block quantity of the CPU reference, with fp32 sums along K).
 //
-// Work split.  A workgroup (4 waves) owns 128 tokens x BN weight rows (BN = 128 or 64); each wave
-// a 64 x BN/2 quarter of 32x32 MFMA tiles.  Each thread unpacks BN of the 256 weights of one
-// weight row into the two LDS planes (rows of 256 B, 16-B chunks XOR-swizzled by row so that 16
-// consecutive rows hit distinct banks); the planes are double-buffered, so the next super-block
-// is unpacked while the MFMAs of the current one run, with one barrier per super-block.
+// Work split.  A workgroup (4 waves) owns 128 tokens x 64 weight rows; each wave 64 tokens x 32
+// rows (two 32x32 MFMA tiles).  Each thread unpacks 64 of the 256 weights of one weight row into
+// the two LDS planes (rows of 256 B, 16-B chunks XOR-swizzled by row so that 16 consecutive rows
+// hit distinct banks); the planes are double-buffered, so the next super-block is unpacked while
+// the MFMAs of the current one run, with one barrier per super-block.  A workgroup takes 80 KB of
+// LDS and its waves at most 256 VGPRs, so two workgroups share a CU: each SIMD runs two waves and
+// one wave's VALU work (unpack, epilogue) issues while the other's MFMAs run.
 //
 // Activation fragments.  An MFMA A operand holds 16 bytes of each of 32 token rows, so reading
 // it straight from Q8_K rows touches 32-64 cache lines per load instruction, for every weight
 // tile.  A first pass (k_q8k_frag) rewrites the quants once into fragment order,
 //   frag[m/32][g][ks 0..7][lane 0..63][16 B] = qs bytes 32ks + 16(lane/32) .. +15 of row 32(m/32) + lane%32,
-// so each A load is one contiguous 1 KB; rows are padded to a multiple of 128 with zeros.  This
+// so each A load is one contiguous 1 KB; rows are padded to a multiple of 256 with zeros.  This
 // needs a caller workspace (kq_gemm_q8k_ws); without one (kq_gemm_q8k, which allocates nothing)
 // the fragments are read from the Q8_K rows directly.  The next super-block's raw weight bytes
 // and activation fragments are loaded one step ahead.  Rows past M or R are clamped for loading
@@ -50,26 +52,8 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int GM_BMAX = 256;  // largest token tile: the fragment workspace is padded to it
 
-#ifndef KQ_GEMM_WN128
-#define KQ_GEMM_WN128 2   // waves along n for 128-row tiles
-#endif
-#ifndef KQ_GEMM_BM256
-#define KQ_GEMM_BM256 0   // 256-token tiles (8 waves, two per SIMD); spills at 256 VGPRs, off
-#endif
-#ifndef KQ_GEMM_IGLP
-// Instruction scheduling of the main loop (all forms give the same bits):
-//   0: compiler order; 1: lo sweep in two tile groups, the first group's epilogue after the second
-//   group's MFMAs; 2: 1 + MFMA/VALU interleave hints in both sweeps; 3: 2 with the hi sweep left to
-//   iglp_opt(1); 4: 1 + the unpack of the next super-block woven between the hi-sweep K steps.
-// Measured (us, Q4_K 12288x4096 / Q6_K 4096x12288 at M = 512, 2048): 0: 98/411/128/397,
-// 1: 92/367/120/397, 2: 85/361/104/377, 3: 79-87/343/96/369, 4: 94/331/116/379.
-#define KQ_GEMM_IGLP 3
-#endif
-#ifndef KQ_GEMM_VPM
-#define KQ_GEMM_VPM 5     // VALU instructions scheduled per MFMA in the hi sweep (unpack of the next super-block)
-#endif
-#ifndef KQ_GEMM_VPM2
-#define KQ_GEMM_VPM2 7    // VALU instructions per MFMA in the second lo-sweep group (first group's epilogue)
+#ifndef KQ_GEMM_LO_VPM
+#define KQ_GEMM_LO_VPM 7  // VALU instructions placed after each MFMA of the second lo-sweep tile (epilogue of the first)
 #endif
 
 // Byte offset of 16-byte chunk `c` (0..15) of LDS plane row `r`: rows are 256 B, the chunk index
@@ -150,26 +134,20 @@ __device__ __forceinline__ void load_raw(RawW<TYPE_Q6_K, PPR>& r, const uint8_t*
     r.dw = ld4(b4 + 208);
 }
 
-// Unpack into LDS buffer Lb, weight row `row` (0..BN-1).  The work comes in UNPACK_PIECES pieces;
-// `only` selects one of them (-1: all), so the kernel can spread the unpack between MFMAs.
-constexpr int UNPACK_PIECES = 4;
+// Unpack into LDS buffer Lb, weight row `row` (0..BN-1).
 template <int PPR, int BN, int BM>
-__device__ __forceinline__ void unpack(const RawW<TYPE_Q4_K, PPR>& r, int pi, int row, GemmBuf<BN, BM>& Lb,
-                                       int only = -1) {
+__device__ __forceinline__ void unpack(const RawW<TYPE_Q4_K, PPR>& r, int pi, int row, GemmBuf<BN, BM>& Lb) {
     constexpr int NPP = RawW<TYPE_Q4_K, PPR>::NPP;
-    constexpr int PER = 2 * NPP / UNPACK_PIECES > 0 ? 2 * NPP / UNPACK_PIECES : 1;   // (pp, c) steps per piece
     int8_t* wh = Lb.wh;
     int8_t* wl = Lb.wl;
 #pragma unroll
     for (int pp = 0; pp < NPP; pp++) {
-        if (only >= 0 && only != (2 * pp) / PER && only != (2 * pp + 1) / PER) continue;
         const int p = pi * NPP + pp;
         const ScMin sm = q4k_scmin_pair(r.hdr.y, r.hdr.z, r.hdr.w, p);
         const uint32_t alo = (sm.sc_lo >> 3) * 0x10001u, blo = (sm.sc_lo & 7u) * 0x10001u;
         const uint32_t ahi = (sm.sc_hi >> 3) * 0x10001u, bhi = (sm.sc_hi & 7u) * 0x10001u;
 #pragma unroll
         for (int c = 0; c < 2; c++) {          // elements 64p + 16c + 0..15 (lo), 64p + 32 + 16c (hi)
-            if (only >= 0 && only != (2 * pp + c) / PER) continue;
             const u32x4 v = r.q[2 * pp + c];
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
             uint32_t h0[4], l0[4], h1[4], l1[4];
@@ -187,24 +165,18 @@ __device__ __forceinline__ void unpack(const RawW<TYPE_Q4_K, PPR>& r, int pi, in
             st16(wh + swz(row, c1), h1[0], h1[1], h1[2], h1[3]);
             st16(wl + swz(row, c1), l1[0], l1[1], l1[2], l1[3]);
         }
-        if (only < 0 || only == (2 * pp + 1) / PER) {
-            const float mlo = (float)sm.m_lo, mhi = (float)sm.m_hi;
-            Lb.wmin[row * 8 + p] = pk_f16(-64.0f * mlo, -64.0f * mhi);
-            Lb.wmin[row * 8 + 4 + p] = pk_f16(-mlo, -mhi);
-        }
+        const float mlo = (float)sm.m_lo, mhi = (float)sm.m_hi;
+        Lb.wmin[row * 8 + p] = pk_f16(-64.0f * mlo, -64.0f * mhi);
+        Lb.wmin[row * 8 + 4 + p] = pk_f16(-mlo, -mhi);
     }
     // every part of the row stores the same d / dmin: no branch in the main loop
-    if (only < 0 || only == UNPACK_PIECES - 1) {
-        Lb.d[row] = f16_lo(r.hdr.x);
-        Lb.dm[row] = f16_hi(r.hdr.x);
-    }
+    Lb.d[row] = f16_lo(r.hdr.x);
+    Lb.dm[row] = f16_hi(r.hdr.x);
 }
 
 template <int PPR, int BN, int BM>
-__device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, int row, GemmBuf<BN, BM>& Lb,
-                                       int only = -1) {
+__device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, int row, GemmBuf<BN, BM>& Lb) {
     constexpr int NJ = RawW<TYPE_Q6_K, PPR>::NJ;
-    constexpr int PER = 4 * NJ / UNPACK_PIECES;                  // (j, k) steps per piece
     const int h = NJ == 2 ? pi : pi >> 1, jj0 = NJ == 2 ? 0 : pi & 1;
     int8_t* wh = Lb.wh;
     int8_t* wl = Lb.wl;
@@ -213,7 +185,6 @@ __device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, in
     const uint32_t s1 = __builtin_amdgcn_alignbyte(r.sce, r.sc.y, sh);    // scales 8h+4 .. 8h+7
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        if (only >= 0 && only / (4 / PER) != j) continue;
         const int jj = jj0 + j;
         uint32_t Lw[2][4], Hw[4];
 #pragma unroll
@@ -233,7 +204,6 @@ __device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, in
         }
 #pragma unroll
         for (int k = 0; k < 4; k++) {              // elements 128h + 32k + 16jj + 0..15
-            if (only >= 0 && only != (4 * j + k) / PER) continue;
             const uint32_t scw = k < 2 ? s0 : s1;
             const int sc = (int)(int8_t)(uint8_t)(scw >> (8 * ((2 * k + jj) & 3)));
             const uint32_t s2 = (uint32_t)(sc & 0xffff) * 0x10001u;
@@ -257,8 +227,7 @@ __device__ __forceinline__ void unpack(const RawW<TYPE_Q6_K, PPR>& r, int pi, in
             st16(wl + swz(row, ch), lb[0], lb[1], lb[2], lb[3]);
         }
     }
-    if (only < 0 || only == UNPACK_PIECES - 1)
-        Lb.d[row] = f16_lo(r.dw >> (8 * sh));   // same value from every part of the row
+    Lb.d[row] = f16_lo(r.dw >> (8 * sh));   // same value from every part of the row
 }
 
 // ------------------------------------------------------------------ activation side
@@ -301,9 +270,9 @@ __device__ __forceinline__ void stage_x(const RawX<XP>& r, int mr, int xp, GemmB
 }
 
 // ------------------------------------------------------------------ the kernel
-// WN waves along n (2 or 4) times WM (2 or 4) along m; each wave owns 64 tokens x BN/WN weight
-// rows, the workgroup BM = 64*WM tokens.  FRAG: A operands from the fragment-order copy XF, else
-// straight from the Q8_K rows XQ.
+// WN waves along n times WM along m; each wave owns 64 tokens x 32 weight rows (two 32x32 MFMA
+// tiles), the workgroup BM = 64*WM tokens x BN = 32*WN rows.  FRAG: A operands from the
+// fragment-order copy XF, else straight from the Q8_K rows XQ.
 template <int TYPE, int BN, int WN, int WM, bool FRAG>
 __global__ void __launch_bounds__(64 * WN * WM)
 k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restrict__ XQ,
@@ -317,7 +286,7 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     constexpr int XP = NTHR / BM;                 // staging parts per activation row
     constexpr int SHIFT = TYPE == TYPE_Q4_K ? 3 : 8;
     static_assert(PPR == 2 || PPR == 4, "a weight row is split in 2 or 4 parts");
-    static_assert(NT >= 1, "at least one 32-row tile per wave");
+    static_assert(NT == 1, "one 32-row tile column per wave");
     __shared__ __attribute__((aligned(16))) GemmBuf<BN, BM> LB0;
     __shared__ __attribute__((aligned(16))) GemmBuf<BN, BM> LB1;
 
@@ -348,13 +317,11 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     const int pr = n0 + prow < R ? n0 + prow : R - 1;
     const uint8_t* wrow = W + ((int64_t)(pr >> 3) * G * 8 + (pr & 7)) * BS;   // block (pr, g) = wrow + g*8*BS
 
-    float yacc[2][NT][16];
+    float yacc[2][16];
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-            for (int a = 0; a < 16; a++) yacc[mt][nt][a] = 0.0f;
+        for (int a = 0; a < 16; a++) yacc[mt][a] = 0.0f;
 
     // ---- prologue: super-block 0 staged, super-block 1's raw bytes in registers
     RawW<TYPE, PPR> raw;
@@ -375,7 +342,7 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     }
     __syncthreads();
 
-    const int nrow0 = wn * NE + l32;        // this lane's B rows: nrow0 + 32 nt
+    const int nrow0 = wn * NE + l32;        // this lane's B row (weight row within the tile)
     // One super-block step; the LDS buffer index is a compile-time constant (the loop is unrolled
     // by two) so the compiler can tell the next buffer's stores from the current buffer's loads and
     // overlap the unpack with the MFMAs.
@@ -383,31 +350,9 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
         constexpr int cur = decltype(cur_c)::value;
         GemmBuf<BN, BM>& Lc = cur ? LB1 : LB0;   // read this step
         GemmBuf<BN, BM>& Ln = cur ? LB0 : LB1;   // filled for the next step
-
+        const int gn = g + 1 < G ? g + 1 : G - 1;
         const int g2 = g + 2 < G ? g + 2 : G - 1;
-        v16i acc[2][NT];
-#if KQ_GEMM_IGLP >= 4
-        // ---- hi sweep, with the unpack of super-block g+1 into the other buffer woven in: one
-        //      piece after every second K step, each step fenced off so the MFMAs of a K step run
-        //      while the next piece's VALU work issues; then fetch the raw bytes of g+2
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            v4i b[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) b[nt] = *reinterpret_cast<const v4i*>(Lc.wh + swz(nrow0 + 32 * nt, 2 * ks + half));
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt],
-                                                                        ks == 0 ? v16i{} : acc[mt][nt], 0, 0, 0);
-            if (ks & 1) unpack(raw, pi, prow, Ln, ks >> 1);
-            if (ks == 6) stage_x<TYPE>(rx, mr, xp, Ln);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        load_raw(raw, wrow + (int64_t)g2 * 8 * BS, pi);
-        load_x(rx, xstage + (int64_t)g2 * Q8K_BYTES, xp);
-#else
+
         // ---- stage super-block g+1 into the other buffer (last iteration: a harmless repeat),
         //      then fetch the raw bytes of g+2
         unpack(raw, pi, prow, Ln);
@@ -415,167 +360,71 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
         load_raw(raw, wrow + (int64_t)g2 * 8 * BS, pi);
         load_x(rx, xstage + (int64_t)g2 * Q8K_BYTES, xp);
 
-        // ---- main sweeps: I = 2^SHIFT * (A . H) + (A . L)
+        // ---- hi sweep: acc = A . H, interleaved by the scheduler with the unpack above
+        v16i acc[2];
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
-            v4i b[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const int r = nrow0 + 32 * nt;
-                b[nt] = *reinterpret_cast<const v4i*>(Lc.wh + swz(r, 2 * ks + half));
-            }
+            const v4i b = *reinterpret_cast<const v4i*>(Lc.wh + swz(nrow0, 2 * ks + half));
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt],
-                                                                        ks == 0 ? v16i{} : acc[mt][nt], 0, 0, 0);
+                acc[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b, ks == 0 ? v16i{} : acc[mt], 0, 0, 0);
         }
-#endif
-#if KQ_GEMM_IGLP >= 2 && KQ_GEMM_IGLP < 4
-        // hi sweep: one MFMA, then a share of the unpack of super-block g+1 (VALU, LDS stores)
-#if KQ_GEMM_IGLP == 3
         __builtin_amdgcn_iglp_opt(1);
-#else
-#pragma unroll
-        for (int i = 0; i < 8 * NT; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read (B operand)
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, KQ_GEMM_VPM, 0);   // VALU (unpack)
-            __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);   // DS write (unpack)
-        }
-#endif
         __builtin_amdgcn_sched_barrier(0);
-#endif
-        const int gn = g + 1 < G ? g + 1 : G - 1;
 
-        // epilogue of one 32x32 tile of super-block g
-        auto epilogue = [&](int mt, int nt) {
+        // epilogue of token tile mt of super-block g
+        auto epilogue = [&](int mt) {
             f32x4 dxv[4];
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 dxv[q] = *reinterpret_cast<const f32x4*>(&Lc.dx[64 * wm + 32 * mt + 8 * q + 4 * half]);
             const int ml = 64 * wm + 32 * mt + l32;
-            const int nl = nrow0 + 32 * nt;
-            const float dn = Lc.d[nl];
+            const float dn = Lc.d[nrow0];
             if (TYPE == TYPE_Q4_K) {
-                const float dmn = Lc.dm[nl];
-                const v8h bm = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&Lc.wmin[nl * 8 + 4 * half]));
+                const float dmn = Lc.dm[nrow0];
+                const v8h bm = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&Lc.wmin[nrow0 * 8 + 4 * half]));
                 const v8h am = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&Lc.xmin[ml * 8 + 4 * half]));
                 const v16f cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, v16f{}, 0, 0, 0);   // -I2
 #pragma unroll
                 for (int a = 0; a < 16; a++) {
-                    const float t = __builtin_fmaf(dmn, cm[a], __fmul_rn(dn, (float)acc[mt][nt][a]));
-                    yacc[mt][nt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], t, yacc[mt][nt][a]);
+                    const float t = __builtin_fmaf(dmn, cm[a], __fmul_rn(dn, (float)acc[mt][a]));
+                    yacc[mt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], t, yacc[mt][a]);
                 }
             } else {
 #pragma unroll
                 for (int a = 0; a < 16; a++)
-                    yacc[mt][nt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], __fmul_rn(dn, (float)acc[mt][nt][a]),
-                                                     yacc[mt][nt][a]);
+                    yacc[mt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], __fmul_rn(dn, (float)acc[mt][a]), yacc[mt][a]);
             }
         };
-        auto shift = [&](int mt, int nt) {
+
+        // ---- lo sweep: acc = 2^SHIFT acc + A . L, one token tile after the other; the epilogue of
+        //      tile 0 runs under the MFMAs of tile 1, then this step's A fragments are replaced by
+        //      those of super-block g+1
+        v4i b[8];
 #pragma unroll
-            for (int a = 0; a < 16; a++) acc[mt][nt][a] <<= SHIFT;
-        };
-#if KQ_GEMM_IGLP >= 1
-        // lo sweep in two tile groups (NT = 2: by nt, NT = 1: by mt); the epilogue of the first
-        // group runs under the MFMAs of the second
-        if constexpr (NT == 2) {
+        for (int ks = 0; ks < 8; ks++) b[ks] = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0, 2 * ks + half));
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) shift(mt, 0);
+        for (int mt = 0; mt < 2; mt++) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                const v4i b = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0, 2 * ks + half));
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-                    acc[mt][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b, acc[mt][0], 0, 0, 0);
-            }
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) shift(mt, 1);
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                const v4i b = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0 + 32, 2 * ks + half));
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-                    acc[mt][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b, acc[mt][1], 0, 0, 0);
-            }
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) epilogue(mt, 0);
-#if KQ_GEMM_IGLP >= 2
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, KQ_GEMM_VPM2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#endif
+            for (int a = 0; a < 16; a++) acc[mt][a] <<= SHIFT;
 #pragma unroll
             for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-                    afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) epilogue(mt, 1);
-        } else {
-            v4i b[8];
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) b[ks] = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0, 2 * ks + half));
-            shift(0, 0);
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-                acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[0][ks], b[ks], acc[0][0], 0, 0, 0);
-            shift(1, 0);
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-                acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[1][ks], b[ks], acc[1][0], 0, 0, 0);
-            epilogue(0, 0);
-#if KQ_GEMM_IGLP >= 2
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, KQ_GEMM_VPM2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#endif
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-                    afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
-            epilogue(1, 0);
+                acc[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[ks], acc[mt], 0, 0, 0);
         }
-#else
+        epilogue(0);
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
+        for (int i = 0; i < 8; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, KQ_GEMM_LO_VPM, 0);  // VALU (epilogue of tile 0)
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);             // DS read
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) shift(mt, nt);
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            v4i b[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const int r = nrow0 + 32 * nt;
-                b[nt] = *reinterpret_cast<const v4i*>(Lc.wl + swz(r, 2 * ks + half));
-            }
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt], acc[mt][nt], 0, 0, 0);
-            // this K step's A fragments are done: fetch those of super-block g+1
+        for (int ks = 0; ks < 8; ks++)
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
                 afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
-        }
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) epilogue(mt, nt);
-#endif
+        epilogue(1);
         __syncthreads();
     };
     for (int g = 0; g < G; g += 2) {
@@ -584,17 +433,14 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     }
 
     // ---- store
+    const int n = n0 + nrow0;
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int n = n0 + nrow0 + 32 * nt;
+    for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-            for (int a = 0; a < 16; a++) {
-                const int m = m0 + 64 * wm + 32 * mt + (a >> 2) * 8 + half * 4 + (a & 3);
-                if (m < M && n < R) Y[(int64_t)m * ldy + n] = yacc[mt][nt][a];
-            }
-    }
+        for (int a = 0; a < 16; a++) {
+            const int m = m0 + 64 * wm + 32 * mt + (a >> 2) * 8 + half * 4 + (a & 3);
+            if (m < M && n < R) Y[(int64_t)m * ldy + n] = yacc[mt][a];
+        }
 }
 
 
@@ -631,19 +477,11 @@ static void launch_tile(const uint8_t* w, int R, int G, const uint8_t* xq, const
 template <int TYPE>
 static void launch_type(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
                         int64_t ldy, hipStream_t s) {
-    // the largest tile that still gives at least two workgroups per CU in total
-    const int64_t cus = device_cus();
-    const int64_t t256 = (int64_t)((R + 127) / 128) * ((M + 255) / 256);
-    const int64_t t128 = (int64_t)((R + 127) / 128) * ((M + 127) / 128);
-    if constexpr (KQ_GEMM_BM256) {
-        if (t256 >= 2 * cus) {
-            launch_tile<TYPE, 128, 2, 4>(w, R, G, xq, xf, M, y, ldy, s);
-            return;
-        }
-    }
-    (void)t256;
-    if (t128 >= 2 * cus) launch_tile<TYPE, 128, KQ_GEMM_WN128, 2>(w, R, G, xq, xf, M, y, ldy, s);
-    else launch_tile<TYPE, 64, 2, 2>(w, R, G, xq, xf, M, y, ldy, s);
+    // 128 tokens x 64 weight rows per workgroup of 4 waves (80 KB of LDS, at most 256 VGPRs), so two
+    // workgroups share a CU and each SIMD holds two waves: one wave's unpack and epilogue run under
+    // the other's MFMAs.  (Measured against 128 x 128 tiles, one wave per SIMD, 4-8 waves per
+    // workgroup: 289-317 against 331-379 us at M = 2048.)
+    launch_tile<TYPE, 64, 2, 2>(w, R, G, xq, xf, M, y, ldy, s);
 }
 
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,

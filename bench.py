@@ -78,6 +78,16 @@ class Runner:
         L = (C.c_int64 * n)(*[m[1] for m in mats])
         self.check(self.lib.kq_gemv_q8k_multi(n, W, Rs, mats[0][2], Ts, C.c_void_p(xq.data_ptr()), 1, Y, L, s))
 
+    def rms_q8k(self, h, res, w, D, xq, s):
+        """kq_rms_q8k on one row: h += res, xq = Q8_K(RMSNorm(h) * w)."""
+        self.check(self.lib.kq_rms_q8k(C.c_void_p(h.data_ptr()), C.c_void_p(res.data_ptr()), 1,
+                                       C.c_void_p(w.data_ptr()), D, 1, D, None, C.c_void_p(xq.data_ptr()), s))
+
+    def swiglu_q8k(self, g, u, n, xq, s):
+        """kq_swiglu_q8k on one row: xq = Q8_K(silu(g) * u)."""
+        self.check(self.lib.kq_swiglu_q8k(C.c_void_p(g.data_ptr()), C.c_void_p(u.data_ptr()), n, 1, n, None,
+                                          C.c_void_p(xq.data_ptr()), s))
+
     def gemm(self, w, R, C_, ty, xq, M, y, ws, s):
         """kq_gemm_q8k_ws with a preallocated workspace (ws: 256-byte aligned device tensor)."""
         self.check(self.lib.kq_gemm_q8k_ws(C.c_void_p(w.data_ptr()), R, C_, ty, C.c_void_p(xq.data_ptr()), M,
@@ -253,6 +263,58 @@ def batched_extra(torch, rn, dev, steps):
     return out
 
 
+def producers_extra(torch, rn, layers, dev, steps=320):
+    """Decode layer with the fused producers and a real layer's data dependencies: RMSNorm of the
+    residual stream (adding the previous block's output) straight to Q8_K -> q/k/v; quantize the
+    attention output (attention itself is not part of this path: a fixed synthetic vector) -> o;
+    RMSNorm (adding o's output) to Q8_K -> gate/up; SwiGLU of their outputs to Q8_K -> down.
+    Also the latency of one fused producer call (64 back-to-back calls in a graph)."""
+    from kq import quantize as kqq
+    D, F = 4096, 12288
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(D, generator=g).to(dev)
+    w_attn = (1 + 0.1 * torch.randn(D, generator=g)).to(dev)
+    w_ffn = (1 + 0.1 * torch.randn(D, generator=g)).to(dev)
+    att = torch.from_numpy(kqq.synthetic_activations(1, D, seed=77)[0]).to(dev)
+    xa, xo, xf = [torch.empty((D // 256) * Q8K, dtype=torch.uint8, device=dev) for _ in range(3)]
+    xd = torch.empty((F // 256) * Q8K, dtype=torch.uint8, device=dev)
+    ys = {name: torch.zeros(R, device=dev) for name, R, _, _, _ in LAYER}
+
+    def step(lay, s):
+        rn.rms_q8k(h, ys["ffn_down"], w_attn, D, xa, s)
+        rn.gemv_multi([(lay[n], R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == 0], xa,
+                      [ys[n] for n, R, C2, ty, sl in LAYER if sl == 0], s)
+        rn.quantize(att, D, xo, s)
+        rn.gemv(lay["attn_output"], 4096, D, 12, xo, 1, ys["attn_output"], s)
+        rn.rms_q8k(h, ys["attn_output"], w_ffn, D, xf, s)
+        rn.gemv_multi([(lay[n], R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == 2], xf,
+                      [ys["ffn_gate"], ys["ffn_up"]], s)
+        rn.swiglu_q8k(ys["ffn_gate"], ys["ffn_up"], F, xd, s)
+        rn.gemv(lay["ffn_down"], 4096, F, 14, xd, 1, ys["ffn_down"], s)
+
+    def run_all():
+        s = rn.stream()
+        for lay in layers:
+            step(lay, s)
+
+    gr = capture(torch, run_all)
+    time_graphs(torch, [gr] * 2)
+    reps = max(1, steps // len(layers))
+    per = time_graphs(torch, [gr] * reps) / (reps * len(layers))
+    wbytes_layer = sum(wbytes(R, C_, ty) for _, R, C_, ty, _ in LAYER)
+    out = {"layer_us": round(per * 1e6, 2), "weight_GB/s": round(wbytes_layer / per / 1e9, 1)}
+
+    def single(fn):
+        gs = capture(torch, lambda: [fn(rn.stream()) for _ in range(64)])
+        time_graphs(torch, [gs] * 2)
+        return round(time_graphs(torch, [gs] * 5) / (5 * 64) * 1e6, 2)
+
+    out["rms_q8k_4096_us"] = single(lambda s: rn.rms_q8k(h, ys["attn_output"], w_ffn, D, xf, s))
+    out["swiglu_q8k_12288_us"] = single(lambda s: rn.swiglu_q8k(ys["ffn_gate"], ys["ffn_up"], F, xd, s))
+    out["q8k_quantize_12288_us"] = single(lambda s: rn.quantize(ys["ffn_gate"], F, xd, s))
+    return out
+
+
 def gemm_extra(torch, rn, dev, timed=True):
     """Prefill GEMM: M in {512, 2048}; 12288x4096 Q4_K and 4096x12288 Q6_K (timed=False: two
     direct calls per shape, for counter runs)."""
@@ -403,6 +465,8 @@ def main():
     if not a.no_extras:
         log("bench: batched GEMV")
         result["batched_gemv"] = batched_extra(torch, rn, dev, 160)
+        log("bench: fused producers")
+        result["producers"] = producers_extra(torch, rn, layers, dev)
         log("bench: prefill GEMM")
         result["prefill_gemm"] = gemm_extra(torch, rn, dev)
         del layers

@@ -68,6 +68,32 @@ int kq_gemv_multi(int n, const void* const* w, const int* R, int C, const int* t
 int kq_q8k_quantize(const float* x, int64_t ldx, int C, int N, void* xq, void* stream);
 
 /*
+ * RMSNorm producing the GEMV input directly in Q8_K: for each of N rows (row stride ld floats),
+ * if add: h += residual (written back to h); s = 1 / sqrtf((float)(sum h^2 / D) + 1e-6f) with the
+ * squares summed in double; xn = (h * s) * w; xq = Q8_K(xn) (as kq_q8k_quantize).  Replaces the
+ * Q4 engine's q4_rms(h, residual, w, xn, xp, D, add) (scripts/kindi_q4/kindi/q4.cu:39-46, launched
+ * by Engine.rmsfold, gpu4.py:104-106) followed by the quantization of xp; the double sum follows
+ * that kernel's order (256 strided partial sums, then a halving tree), so h and xn are
+ * bit-identical to it.  The CPU engine's rmsfold (kcpu4.c:123-139) is the same computation with a
+ * sequential double sum.  D % 256 == 0, D <= 16384; xn may be NULL (only xq is produced) or h itself;
+ * residual (read only when add != 0) must not overlap h.  All pointers 4-byte aligned.
+ */
+int kq_rms_q8k(float* h, const float* residual, int add, const float* w, int D, int N, int64_t ld, float* xn,
+               void* xq, void* stream);
+
+/*
+ * SwiGLU producing the down-projection input directly in Q8_K: y = (g / (1 + exp(-g))) * u
+ * elementwise for N rows of n values (row stride ld floats), xq = Q8_K(y).  Replaces q4_silu
+ * (q4.cu:36-38, launched as k_smfold by the FFN, engine.py:287) and the CPU engine's
+ * silu(ffg) * ffu (kcpu4.c:77, 292) followed by the quantization.  exp is the library's own
+ * binary32 exp (within 2 ulp of the exact value, like CUDA's and glibc's expf), so y agrees with
+ * the reference to a few ulp and exactly with the repository's CPU oracle.  n % 256 == 0; y may
+ * be NULL.  All pointers 4-byte aligned.
+ */
+int kq_swiglu_q8k(const float* gate, const float* up, int n, int N, int64_t ld, float* y, void* xq,
+                  void* stream);
+
+/*
  * Y[n][r] (row stride ldy floats) for N = 1..16 Q8_K activation rows: batch-1 decode (N = 1)
  * and speculative-verify GEMV.  Same role as q4_gemv with quantized activations; the batched
  * form follows the ternary engine's k_tc_mv{2,4,8}(..., y[ntok][R]) (tc.cu:306-310).

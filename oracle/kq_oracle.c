@@ -20,7 +20,10 @@
  *     and ggml_vec_dot_q6_K_q8_K generic versions, same commit), exposed per sub-block,
  *     and the output evaluated in double from those exact integers;
  *   - the same GGML dot with GGML's own fp32 accumulation order (8 partial lanes),
- *     kept to show that the double evaluation and GGML's fp32 one agree to tolerance.
+ *     kept to show that the double evaluation and GGML's fp32 one agree to tolerance;
+ *   - the producers of the GEMV inputs: RMSNorm with residual add (q4_rms, q4.cu:39-46,
+ *     and the CPU engine's rmsfold, kcpu4.c:123-139) and SwiGLU (q4_silu, q4.cu:36-38;
+ *     kcpu4.c:77, 292), with a binary32 exp built from IEEE single operations.
  *
  * Build: gcc -O2 -ffp-contract=off -fopenmp -shared -fPIC (oracle/Makefile).
  */
@@ -319,4 +322,69 @@ void kqo_gemv_q8k_ggml(const uint8_t* W, int R, int C, int type, const uint8_t* 
     for (int n = 0; n < N; n++)
         for (int r = 0; r < R; r++)
             y[(size_t)n * ldy + r] = kqo_dot_q8k_ggml(W, C, type, r, xq + (size_t)n * G * Q8K_BYTES);
+}
+
+/* ------------------------------------------------------------------ producers of the GEMV inputs */
+
+/* exp(x) in binary32 from IEEE single operations in a fixed order: Cody-Waite reduction
+ * r = x - n ln2 (ln2 split in 0x1.62e4p-1, whose 15 significant bits make n * it exact, and
+ * 0x1.7f7d1cp-20), e^r by its degree-7 Taylor polynomial in Horner form (|r| <= ln2/2, truncation
+ * below 0.1 ulp), then exact scaling by 2^n (two steps below the normal range, one rounding).
+ * The library's kernels evaluate the same steps, so both give the same bits.  Compiled with
+ * -ffp-contract=off: no step is fused. */
+static float pow2i(int k) { uint32_t u = (uint32_t)(k + 127) << 23; float f; memcpy(&f, &u, 4); return f; }
+
+float kqo_expf(float x) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep+6f) return INFINITY;
+    if (x < -0x1.9fe368p+6f) return 0.0f;
+    const float n = rintf(x * 0x1.715476p+0f);
+    const float r = (x - n * 0x1.62e4p-1f) - n * 0x1.7f7d1cp-20f;
+    float p = 0x1.a01a02p-13f;
+    p = p * r + 0x1.6c16c2p-10f;
+    p = p * r + 0x1.111112p-7f;
+    p = p * r + 0x1.555556p-5f;
+    p = p * r + 0x1.555556p-3f;
+    p = p * r + 0x1p-1f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    int k = (int)n;
+    if (k > 127) { p = p * 2.0f; k -= 1; }
+    if (k < -126) return (p * pow2i(k + 64)) * 0x1p-64f;
+    return p * pow2i(k);
+}
+
+/* q4_rms (scripts/kindi_q4/kindi/q4.cu:39-46) for one row: optional residual add into h, sum of
+ * squares in double in that kernel's order (thread t of 256 adds i = t, t+256, ... in sequence,
+ * then sums[t] += sums[t+n] for n = 128, 64, ..., 1), s = 1/sqrtf((float)(sum/D) + 1e-6f),
+ * xn = (h*s)*w.  order = 1 sums sequentially instead, as the CPU engine's rmsfold does
+ * (kcpu4.c:123-139). */
+void kqo_rms_norm(float* h, const float* res, int add, const float* w, int D, float* xn, int order) {
+    double acc;
+    if (add) for (int i = 0; i < D; i++) h[i] = h[i] + res[i];
+    if (order == 1) {
+        acc = 0.0;
+        for (int i = 0; i < D; i++) acc += (double)h[i] * (double)h[i];
+    } else {
+        double sums[256];
+        for (int t = 0; t < 256; t++) {
+            double s = 0.0;
+            for (int i = t; i < D; i += 256) s += (double)h[i] * (double)h[i];
+            sums[t] = s;
+        }
+        for (int n = 128; n; n >>= 1)
+            for (int t = 0; t < n; t++) sums[t] += sums[t + n];
+        acc = sums[0];
+    }
+    const float s = 1.0f / sqrtf((float)(acc / D) + 1e-6f);
+    for (int i = 0; i < D; i++) xn[i] = (h[i] * s) * w[i];
+}
+
+/* silu(g) * u (q4_silu, q4.cu:36-38; kcpu4.c:77, 292) with kqo_expf. */
+void kqo_swiglu(const float* g, const float* u, int64_t n, float* y) {
+    for (int64_t i = 0; i < n; i++) y[i] = (g[i] / (1.0f + kqo_expf(-g[i]))) * u[i];
+}
+
+void kqo_expf_n(const float* x, int64_t n, float* y) {
+    for (int64_t i = 0; i < n; i++) y[i] = kqo_expf(x[i]);
 }

@@ -54,6 +54,11 @@ def lib():
         L.kqo_subblock_sums.argtypes = [_PU8, C.c_int, C.c_int, C.c_int, _PU8, C.c_int, _PI32]
         L.kqo_gemv_q8k.argtypes = [_PU8, C.c_int, C.c_int, C.c_int, _PU8, C.c_int, _PD, C.c_int64]
         L.kqo_gemv_q8k_ggml.argtypes = [_PU8, C.c_int, C.c_int, C.c_int, _PU8, C.c_int, _PF, C.c_int64]
+        L.kqo_expf.argtypes = [C.c_float]
+        L.kqo_expf.restype = C.c_float
+        L.kqo_rms_norm.argtypes = [_PF, _PF, C.c_int, _PF, C.c_int, _PF, C.c_int]
+        L.kqo_swiglu.argtypes = [_PF, _PF, C.c_int64, _PF]
+        L.kqo_expf_n.argtypes = [_PF, C.c_int64, _PF]
         _lib = L
     return _lib
 
@@ -173,4 +178,39 @@ def ref_dequant_row(W, R, C_, ty, row):
     m, keep = ref_mat(W, R, C_, ty)
     y = np.empty(C_, np.float32)
     ref().kc_dequant(C.byref(m), row, _p(y, _PF))
+    return y
+
+
+# ---------------------------------------------------------------- producers of the GEMV inputs
+def expf(x):
+    """The library's binary32 exp, elementwise (kqo_expf)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().kqo_expf_n(_p(x, _PF), x.size, _p(y, _PF))
+    return y
+
+
+def rms_norm(h, w, residual=None, order=0):
+    """q4_rms per row of h [N][D] (order 0: that kernel's double-sum order; 1: the CPU engine's
+    sequential sum).  Returns (h after the residual add, xn)."""
+    h = np.array(np.atleast_2d(h), np.float32, order="C")
+    w = np.ascontiguousarray(w, np.float32)
+    N, D = h.shape
+    res = None if residual is None else np.ascontiguousarray(np.atleast_2d(residual), np.float32)
+    xn = np.empty_like(h)
+    for n in range(N):
+        hr = h[n].copy()
+        rr = res[n] if res is not None else hr
+        lib().kqo_rms_norm(_p(hr, _PF), _p(np.ascontiguousarray(rr), _PF), 1 if res is not None else 0,
+                           _p(w, _PF), D, _p(xn[n], _PF), order)
+        h[n] = hr
+    return h, xn
+
+
+def swiglu(g, u):
+    """silu(g) * u elementwise (kqo_swiglu)."""
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    y = np.empty_like(g)
+    lib().kqo_swiglu(_p(g, _PF), _p(u, _PF), g.size, _p(y, _PF))
     return y

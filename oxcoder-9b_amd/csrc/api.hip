@@ -107,6 +107,38 @@ int kq_q8k_quantize(const float* x, int64_t ldx, int C, int N, void* xq, void* s
     return check_launch(fn);
 }
 
+int kq_rms_q8k(float* h, const float* residual, int add, const float* w, int D, int N, int64_t ld, float* xn,
+               void* xq, void* stream) {
+    static const char* fn = "kq_rms_q8k";
+    if (D <= 0 || D % 256 || D > 16384)   // the kernel's per-thread row share (RMS_DMAX)
+        return fail(KQ_ERR_ARG, "%s: D=%d must be a positive multiple of 256, at most 16384", fn, D);
+    if (N <= 0 || N > 65535) return fail(KQ_ERR_ARG, "%s: N=%d must be 1..65535", fn, N);
+    if (ld < D) return fail(KQ_ERR_ARG, "%s: ld=%lld is smaller than D=%d", fn, (long long)ld, D);
+    KQ_TRY(check_ptr(h, 4, "h", fn));
+    KQ_TRY(check_ptr(w, 4, "w", fn));
+    KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    if (add) KQ_TRY(check_ptr(residual, 4, "residual", fn));
+    if (xn) KQ_TRY(check_ptr(xn, 4, "xn", fn));
+    launch_rms_q8k(h, add ? residual : nullptr, add ? 1 : 0, w, D, N, ld, xn, static_cast<uint8_t*>(xq),
+                   as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_swiglu_q8k(const float* gate, const float* up, int n, int N, int64_t ld, float* y, void* xq,
+                  void* stream) {
+    static const char* fn = "kq_swiglu_q8k";
+    if (n <= 0 || n % 256) return fail(KQ_ERR_ARG, "%s: n=%d must be a positive multiple of 256", fn, n);
+    if (N <= 0) return fail(KQ_ERR_ARG, "%s: N=%d must be positive", fn, N);
+    if (ld < n) return fail(KQ_ERR_ARG, "%s: ld=%lld is smaller than n=%d", fn, (long long)ld, n);
+    if ((int64_t)N * (n / 256) > 0x7fffffffLL) return fail(KQ_ERR_ARG, "%s: N*n/256 exceeds 2^31-1 blocks", fn);
+    KQ_TRY(check_ptr(gate, 4, "gate", fn));
+    KQ_TRY(check_ptr(up, 4, "up", fn));
+    KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    if (y) KQ_TRY(check_ptr(y, 4, "y", fn));
+    launch_swiglu_q8k(gate, up, n, N, ld, y, static_cast<uint8_t*>(xq), as_stream(stream));
+    return check_launch(fn);
+}
+
 int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, float* y,
                 int64_t ldy, void* stream) {
     static const char* fn = "kq_gemv_q8k";

@@ -26,6 +26,11 @@ inline int block_bytes(int type) { return type == KQ_TYPE_Q4_K ? 144 : 210; }
 
 // Launchers implemented by the kernel translation units.  Arguments are already validated.
 void launch_q8k_quantize(const float* x, int64_t ldx, int C, int N, uint8_t* xq, hipStream_t s);
+// Fused producers of Q8_K activations (RMSNorm with optional residual add; SwiGLU).
+void launch_rms_q8k(float* h, const float* res, int add, const float* w, int D, int N, int64_t ld, float* xn,
+                    uint8_t* xq, hipStream_t s);
+void launch_swiglu_q8k(const float* gate, const float* up, int n, int N, int64_t ld, float* y, uint8_t* xq,
+                       hipStream_t s);
 void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N, float* y,
                      int64_t ldy, int rows_per_wave, hipStream_t s);
 // n (1..3) matrices of one type sharing xq; one launch per group of up to 4 tokens.

@@ -1,0 +1,178 @@
+// Producers of the GEMV inputs for gfx950: RMSNorm and SwiGLU that write the Q8_K activation
+// blocks directly (and, optionally, the fp32 values), so no separate quantizer pass re-reads them.
+//
+// k_rms_q8k follows the Q4 engine's q4_rms (scripts/kindi_q4/kindi/q4.cu:39-46): optional residual
+// add into h, sum of squares in double with the same order (256 strided per-thread sums, then the
+// shared-memory tree), s = 1 / sqrtf((float)(sum / D) + 1e-6f), xn = (h * s) * w.  The square of a
+// float is exact in double and every double addition and the float steps are IEEE, so h, s and xn
+// are bit-identical to that kernel's.  The CPU engine's rmsfold (kcpu4.c:123-139) adds the squares
+// in sequence instead; the two orders give the same float s except when the double sum lies within
+// a few double ulps of a float rounding boundary.
+//
+// k_swiglu_q8k follows q4_silu (q4.cu:36-38) and the CPU engine's FFN (kcpu4.c:77, 292):
+// y = (g / (1 + exp(-g))) * u.  exp is kq_expf below, a binary32 exp built from IEEE single
+// operations in a fixed order (Cody-Waite reduction by ln 2, degree-7 Taylor polynomial in Horner
+// form, exact scaling by 2^n), so the oracle's C copy of the same steps gives the same bits; it is
+// within 2 ulp of the exact exp, as CUDA's and glibc's expf are.
+#include "kq_device.h"
+#include "kq_internal.h"
+#include "q8k_block.h"
+
+namespace kq {
+
+// 2^k as a float for k in [-126, 127].
+__device__ __forceinline__ float pow2i(int k) { return __builtin_bit_cast(float, (uint32_t)(k + 127) << 23); }
+
+__device__ __forceinline__ float kq_expf(float x) {
+    if (x != x) return x + x;                           // NaN
+    if (x > 0x1.62e42ep+6f) return __builtin_inff();    // above the largest x with exp(x) finite
+    if (x < -0x1.9fe368p+6f) return 0.0f;               // exp(x) < 2^-150 rounds to zero
+    const float n = __builtin_rintf(__fmul_rn(x, 0x1.715476p+0f));            // round(x / ln 2)
+    // ln 2 = 0x1.62e4p-1 (15 significant bits: n * it is exact) + 0x1.7f7d1cp-20
+    const float r = __fsub_rn(__fsub_rn(x, __fmul_rn(n, 0x1.62e4p-1f)), __fmul_rn(n, 0x1.7f7d1cp-20f));
+    float p = 0x1.a01a02p-13f;                                  // 1/7!
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.6c16c2p-10f);            // 1/6!
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.111112p-7f);             // 1/5!
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-5f);             // 1/4!
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-3f);             // 1/3!
+    p = __fadd_rn(__fmul_rn(p, r), 0x1p-1f);                    // 1/2!
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    int k = (int)n;                                             // -150 .. 128
+    if (k > 127) { p = __fmul_rn(p, 2.0f); k -= 1; }
+    if (k < -126) return __fmul_rn(__fmul_rn(p, pow2i(k + 64)), 0x1p-64f);   // subnormal: one rounding
+    return __fmul_rn(p, pow2i(k));
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, kq_expf(-g))), u);
+}
+
+// One workgroup of 256 threads per row; J >= D/256 row elements per thread (a compile-time count,
+// so every load is unconditional: elements past D re-read element D-1 and are not used).  Every
+// global load of the row (h, residual, and the w values of pass 2) is issued up front, so the
+// kernel waits for memory once.  Dynamic LDS holds the row (D floats) between the two passes.
+template <int J>
+__global__ void __launch_bounds__(256)
+k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int D, int64_t ld, float* xn,
+          uint8_t* __restrict__ xq) {
+    constexpr int B = (J + 3) / 4;             // Q8_K blocks per wave, at most
+    extern __shared__ float hrow[];            // D floats
+    __shared__ double sums[128];
+    __shared__ float s_sh;
+    const int t = threadIdx.x, row = blockIdx.x;
+    const int lane = t & 63, wv = t >> 6;
+    const int G = D / QK;
+    float* hr = h + (int64_t)row * ld;
+    const float* rr = res + (int64_t)row * ld;
+    auto at = [&](int k) { const int i = t + 256 * k; return i < D ? i : D - 1; };
+
+    float v[J];
+#pragma unroll
+    for (int k = 0; k < J; k++) v[k] = hr[at(k)];
+    if (add) {
+        float r[J];
+#pragma unroll
+        for (int k = 0; k < J; k++) r[k] = rr[at(k)];
+#pragma unroll
+        for (int k = 0; k < J; k++) v[k] = __fadd_rn(v[k], r[k]);
+    }
+    f32x4 wq[B];                               // pass 2 operands: w of blocks wv, wv + 4, ...
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+        const int g = wv + 4 * b < G ? wv + 4 * b : G - 1;
+        wq[b] = *reinterpret_cast<const f32x4_a4*>(w + g * QK + 4 * lane);
+    }
+
+    // pass 1: thread t's partial sum over i = t, t + 256, ... in sequence (q4.cu:41)
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < J; k++) {
+        if (t + 256 * k < D) {
+            if (add) hr[t + 256 * k] = v[k];
+            hrow[t + 256 * k] = v[k];
+            sum = __dadd_rn(sum, __dmul_rn((double)v[k], (double)v[k]));
+        }
+    }
+    // the halving tree of q4.cu:42-43: sums[t] += sums[t + n] for n = 128, 64, ..., 1
+    if (t >= 128) sums[t - 128] = sum;
+    __syncthreads();
+    if (t < 128) sum = __dadd_rn(sum, sums[t]);                 // n = 128
+    __syncthreads();
+    if (t >= 64 && t < 128) sums[t - 64] = sum;
+    __syncthreads();
+    if (t < 64) {
+        sum = __dadd_rn(sum, sums[t]);                           // n = 64
+#pragma unroll
+        for (int n = 32; n; n >>= 1) sum = __dadd_rn(sum, __shfl_down(sum, n, 64));   // lane t += lane t + n
+        if (t == 0) {
+            // sqrtf correctly rounded: the double square root of a float, rounded to float, is
+            // (53 >= 2*24 + 2 bits), while v_sqrt_f32 alone is not
+            const float ms = __fadd_rn((float)__ddiv_rn(sum, (double)D), 1e-6f);
+            s_sh = __fdiv_rn(1.0f, (float)__dsqrt_rn((double)ms));
+        }
+    }
+    __syncthreads();
+    const float s = s_sh;
+
+    // pass 2: Q8_K blocks; wave wv takes blocks wv, wv + 4, ...; lane l the values 4l .. 4l+3.
+    // xn may be h itself: the values now come from LDS.
+    float* xr = xn ? xn + (int64_t)row * ld : nullptr;
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+        const int g = wv + 4 * b;
+        if (g >= G) break;
+        const int i0 = g * QK + 4 * lane;
+        const f32x4 hv = *reinterpret_cast<const f32x4*>(hrow + i0);
+        float e[4];
+        e[0] = __fmul_rn(__fmul_rn(hv.x, s), wq[b].x);
+        e[1] = __fmul_rn(__fmul_rn(hv.y, s), wq[b].y);
+        e[2] = __fmul_rn(__fmul_rn(hv.z, s), wq[b].z);
+        e[3] = __fmul_rn(__fmul_rn(hv.w, s), wq[b].w);
+        if (xr) *reinterpret_cast<f32x4_a4*>(xr + i0) = f32x4{e[0], e[1], e[2], e[3]};
+        q8k_block_store(e, lane, xq + ((int64_t)row * G + g) * Q8K_BYTES);
+    }
+}
+
+// One wave per 256-value block.
+__global__ void __launch_bounds__(256)
+k_swiglu_q8k(const float* __restrict__ gate, const float* __restrict__ up, int G, int64_t ld, int nblocks,
+             float* __restrict__ y, uint8_t* __restrict__ xq) {
+    const int lane = threadIdx.x & 63;
+    const int blk = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (blk >= nblocks) return;
+    const int n = blk / G, g = blk - n * G;
+    const int64_t i0 = (int64_t)n * ld + (int64_t)g * QK + 4 * lane;
+    const f32x4 gv = *reinterpret_cast<const f32x4_a4*>(gate + i0);
+    const f32x4 uv = *reinterpret_cast<const f32x4_a4*>(up + i0);
+    float e[4];
+    e[0] = silu_mul(gv.x, uv.x);
+    e[1] = silu_mul(gv.y, uv.y);
+    e[2] = silu_mul(gv.z, uv.z);
+    e[3] = silu_mul(gv.w, uv.w);
+    if (y) *reinterpret_cast<f32x4_a4*>(y + i0) = f32x4{e[0], e[1], e[2], e[3]};
+    q8k_block_store(e, lane, xq + (int64_t)blk * Q8K_BYTES);
+}
+
+void launch_rms_q8k(float* h, const float* res, int add, const float* w, int D, int N, int64_t ld, float* xn,
+                    uint8_t* xq, hipStream_t s) {
+    const size_t lds = (size_t)D * sizeof(float);
+    const int j = (D + 255) / 256;             // row elements per thread: 1 .. 64 (D <= 16384)
+    const dim3 grid(N), block(256);
+    const float* r = res ? res : h;
+    if (j <= 4) hipLaunchKernelGGL(k_rms_q8k<4>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
+    else if (j <= 8) hipLaunchKernelGGL(k_rms_q8k<8>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
+    else if (j <= 16) hipLaunchKernelGGL(k_rms_q8k<16>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
+    else if (j <= 32) hipLaunchKernelGGL(k_rms_q8k<32>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
+    else if (j <= 48) hipLaunchKernelGGL(k_rms_q8k<48>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
+    else hipLaunchKernelGGL(k_rms_q8k<64>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
+}
+
+void launch_swiglu_q8k(const float* gate, const float* up, int n, int N, int64_t ld, float* y, uint8_t* xq,
+                       hipStream_t s) {
+    const int G = n / QK, nblocks = N * G, wpb = 4;
+    hipLaunchKernelGGL(k_swiglu_q8k, dim3((nblocks + wpb - 1) / wpb), dim3(64 * wpb), 0, s, gate, up, G, ld,
+                       nblocks, y, xq);
+}
+
+}  // namespace kq

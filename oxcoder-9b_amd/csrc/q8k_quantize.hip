@@ -1,11 +1,8 @@
-// Q8_K activation quantizer for gfx950: one wave per 256-value block, 4 values per lane.
-//
-// Semantics (GGML quantize_row_q8_K_ref): max = signed value of the first element with the
-// largest |x|; iscale = -127/max; q = min(127, round-half-even(iscale*x)); d = 1/iscale;
-// bsums[k] = sum of q[16k..16k+15]; an all-zero block gives d = 0, q = 0, bsums = 0.
-// Division is IEEE (hipcc default), so d and the quants match the CPU bit for bit.
+// Q8_K activation quantizer for gfx950: one wave per 256-value block, 4 values per lane
+// (block quantization in q8k_block.h).
 #include "kq_device.h"
 #include "kq_internal.h"
+#include "q8k_block.h"
 
 namespace kq {
 
@@ -15,58 +12,9 @@ k_q8k_quantize(const float* __restrict__ x, int64_t ldx, int G, int nblocks, uin
     const int blk = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     const int n = blk / G, g = blk - n * G;
-    const float* xb = x + (int64_t)n * ldx + (int64_t)g * QK + 4 * lane;
-    const f32x4 v = *reinterpret_cast<const f32x4_a4*>(xb);
-
-    // max |x| over the block: butterfly max (exact, order-free); NaN never wins (v_max returns
-    // the other operand), matching the strict "ax > amax" scan of the reference definition.
+    const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + (int64_t)n * ldx + (int64_t)g * QK + 4 * lane);
     const float e[4] = {v.x, v.y, v.z, v.w};
-    float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(e[0]), __builtin_fabsf(e[1])),
-                                 __builtin_fmaxf(__builtin_fabsf(e[2]), __builtin_fabsf(e[3])));
-    amax = __builtin_fmaxf(amax, dppf<DPP_QUAD_XOR1>(amax));
-    amax = __builtin_fmaxf(amax, dppf<DPP_QUAD_XOR2>(amax));
-    amax = __builtin_fmaxf(amax, dppf<DPP_ROW_HALF_MIRROR>(amax));
-    amax = __builtin_fmaxf(amax, dppf<DPP_ROW_MIRROR>(amax));
-    amax = __builtin_fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, amax), SWZ_XOR16)));
-    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, 64));
-    // signed value of the first element with |x| == amax: lowest lane holding one, lowest k in it
-    float first = 0.0f;
-    bool has = false;
-#pragma unroll
-    for (int k = 3; k >= 0; k--)
-        if (__builtin_fabsf(e[k]) == amax) { first = e[k]; has = true; }
-    const uint64_t holders = __ballot(has);
-    const int src = holders ? __builtin_ctzll(holders) : 0;
-    const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, first), src));
-
-    uint8_t* ob = xq + (int64_t)blk * Q8K_BYTES;
-    uint32_t packed = 0;
-    int s4 = 0;
-    float d = 0.0f;
-    if (amax != 0.0f) {
-        const float iscale = -127.0f / vmax;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float t = __fmul_rn(iscale, e[k]);
-            int q = (int)__builtin_rintf(t);
-            q = q < 127 ? q : 127;
-            s4 += q;
-            packed |= (uint32_t)(q & 0xff) << (8 * k);
-        }
-        d = 1.0f / iscale;
-    }
-    // 16-value sums: lanes 4j..4j+3 hold values 16j..16j+15.
-    s4 = quad_sum_i32(s4);
-    // Pack two adjacent sums (lanes 8k and 8k+4 hold sums 2k, 2k+1) into one dword for the store:
-    // lane 8k reads lane 8k+7 through the half-row mirror.
-    const int s_next = dpp<DPP_ROW_HALF_MIRROR>(s4);
-
-    *reinterpret_cast<uint32_t*>(ob + 4 + 4 * lane) = packed;
-    if (lane == 0) *reinterpret_cast<float*>(ob) = d;
-    if ((lane & 7) == 0) {
-        const uint32_t pair = ((uint32_t)s4 & 0xffffu) | ((uint32_t)s_next << 16);
-        *reinterpret_cast<uint32_t*>(ob + 260 + 4 * (lane >> 3)) = pair;
-    }
+    q8k_block_store(e, lane, xq + (int64_t)blk * Q8K_BYTES);
 }
 
 void launch_q8k_quantize(const float* x, int64_t ldx, int C, int N, uint8_t* xq, hipStream_t s) {

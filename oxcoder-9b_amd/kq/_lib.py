@@ -18,6 +18,8 @@ KQ_SYMBOLS = {
     "kq_gemv": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "kq_gemv_multi": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, C.POINTER(_vp), _vp]),
     "kq_q8k_quantize": (_i, [_vp, _i64, _i, _i, _vp, _vp]),
+    "kq_rms_q8k": (_i, [_vp, _vp, _i, _vp, _i, _i, _i64, _vp, _vp, _vp]),
+    "kq_swiglu_q8k": (_i, [_vp, _vp, _i, _i, _i64, _vp, _vp, _vp]),
     "kq_gemv_q8k": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),
     "kq_gemv_q8k_multi": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, _i,
                                C.POINTER(_vp), C.POINTER(_i64), _vp]),

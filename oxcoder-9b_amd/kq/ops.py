@@ -61,6 +61,61 @@ def q8k_quantize(x, out=None):
     return out
 
 
+def _rows(x, name):
+    """[N][n] fp32 device rows (1-D: one row) with contiguous rows; returns (2-D view, N, n, ld)."""
+    if x.dim() == 1:
+        x = x.unsqueeze(0)
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("%s must be [N][n] with contiguous rows" % name)
+    _dev(x, name, torch.float32)
+    return x, x.shape[0], x.shape[1], x.stride(0)
+
+
+def _q8k_out(xq, N, n, device):
+    if xq is None:
+        return torch.empty((N, n // QK * Q8K_BYTES), dtype=torch.uint8, device=device)
+    if xq.numel() < N * (n // QK) * Q8K_BYTES:
+        raise ValueError("xq too small for %d Q8_K rows of %d" % (N, n))
+    return xq
+
+
+def rms_q8k(h, w, residual=None, xn=None, xq=None):
+    """RMSNorm of the rows of h (in place residual add when ``residual`` is given), writing the
+    Q8_K blocks of xn = (h * s) * w and, if ``xn`` is given, xn itself (kq_rms_q8k; q4_rms,
+    q4.cu:39-46).  Returns (xn, xq)."""
+    h2, N, D, ld = _rows(h, "h")
+    if w.numel() < D:
+        raise ValueError("w must hold D=%d floats" % D)
+    for t, name in ((residual, "residual"), (xn, "xn")):
+        if t is not None:
+            t2, n2, d2, ld2 = _rows(t, name)
+            if (n2, d2, ld2) != (N, D, ld):
+                raise ValueError("%s must have the shape and row stride of h" % name)
+    xq = _q8k_out(xq, N, D, h.device)
+    _lib.check(_lib.kq().kq_rms_q8k(C.c_void_p(h2.data_ptr()),
+                                    C.c_void_p(residual.data_ptr()) if residual is not None else None,
+                                    1 if residual is not None else 0, _dev(w, "w", torch.float32), D, N, ld,
+                                    C.c_void_p(xn.data_ptr()) if xn is not None else None,
+                                    _dev(xq, "xq", torch.uint8), _stream(h.device)))
+    return xn, xq
+
+
+def swiglu_q8k(gate, up, y=None, xq=None):
+    """Q8_K blocks of y = silu(gate) * up and, if ``y`` is given, y itself (kq_swiglu_q8k;
+    q4_silu, q4.cu:36-38).  Returns (y, xq)."""
+    g2, N, n, ld = _rows(gate, "gate")
+    for t, name in ((up, "up"), (y, "y")):
+        if t is not None:
+            t2, n2, d2, ld2 = _rows(t, name)
+            if (n2, d2, ld2) != (N, n, ld):
+                raise ValueError("%s must have the shape and row stride of gate" % name)
+    xq = _q8k_out(xq, N, n, gate.device)
+    _lib.check(_lib.kq().kq_swiglu_q8k(C.c_void_p(g2.data_ptr()), _dev(up, "up", torch.float32), n, N, ld,
+                                       C.c_void_p(y.data_ptr()) if y is not None else None,
+                                       _dev(xq, "xq", torch.uint8), _stream(gate.device)))
+    return y, xq
+
+
 def gemv_q8k(w, R, C_, ty, xq, N, y, ldy=None):
     """Y[n][r] for N Q8_K activation rows (kq_gemv_q8k, N <= 16)."""
     pw = _weights(w, R, C_, ty)

@@ -119,3 +119,20 @@ def test_quantizer_zero_and_constant_blocks(orc):
         deq = orc.dequant(W, 8, 512, ty)
         np.testing.assert_allclose(deq, w, atol=0.5 / 31)
         assert not deq[0].any() and not deq[3:].any()
+
+
+def test_producer_argument_errors():
+    """kq_rms_q8k / kq_swiglu_q8k validate shapes and pointers before any launch."""
+    from kq import _lib
+    lib = _lib.kq()
+    p = ctypes.c_void_p(256)
+    rc = lib.kq_rms_q8k(p, None, 0, p, 300, 1, 300, None, p, None)
+    assert rc == _lib.KQ_ERR_ARG and "D=300" in lib.kq_last_error().decode()
+    rc = lib.kq_rms_q8k(p, None, 1, p, 256, 1, 256, None, p, None)
+    assert rc == _lib.KQ_ERR_ARG and "residual is NULL" in lib.kq_last_error().decode()
+    rc = lib.kq_rms_q8k(p, None, 0, p, 512, 1, 256, None, p, None)
+    assert rc == _lib.KQ_ERR_ARG and "ld=256" in lib.kq_last_error().decode()
+    rc = lib.kq_swiglu_q8k(p, p, 256, 0, 256, None, p, None)
+    assert rc == _lib.KQ_ERR_ARG and "N=0" in lib.kq_last_error().decode()
+    rc = lib.kq_swiglu_q8k(p, None, 256, 1, 256, None, p, None)
+    assert rc == _lib.KQ_ERR_ARG and "up is NULL" in lib.kq_last_error().decode()

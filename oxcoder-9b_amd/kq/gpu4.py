@@ -15,6 +15,11 @@ for each name, ``outs[i][:R] = W_name @ x`` on the current stream, asynchronousl
 ``gemv_batch`` (speculative verify, N <= 16 rows) and ``gemm`` (prefill chunk, any M) extend the
 same contract to several activation rows: X is [N][C] fp32, each out is [N][R] (row stride
 ``out.stride(0)``), the batched layout of the ternary engine's k_tc_mv (tc.cu:306-310).
+
+The producers of the GEMV inputs write the Q8_K activation directly: ``rmsfold_q8k`` (the
+residual add + RMSNorm of Engine.rmsfold, gpu4.py:104-106 / q4_rms, q4.cu:39-46) and
+``swiglu_q8k`` (q4_silu, q4.cu:36-38, as the FFN launches it, engine.py:287); ``gemv_q8`` then
+runs the named matrices on that Q8_K input with no further quantization.
 """
 import torch
 
@@ -86,6 +91,40 @@ class Engine:
         for i in range(0, len(mats), 3):
             ops.gemv_q8k_multi(mats[i:i + 3], xq, 1, list(outs[i:i + 3]))
         return 1
+
+    def gemv_q8(self, names, xq, outs, N=1):
+        """gemv on an activation already in Q8_K (from rmsfold_q8k / swiglu_q8k); returns 1."""
+        mats = [self.w[n] for n in names]
+        if len(outs) < len(mats):
+            raise ValueError("one output per matrix")
+        C = mats[0][2]
+        if any(m[2] != C for m in mats):
+            raise ValueError("matrices sharing xq must have the same column count")
+        if xq.numel() < N * (C // QK) * Q8K_BYTES:
+            raise ValueError("xq holds fewer than %d Q8_K rows of %d" % (N, C))
+        for (w, R, _, _), y in zip(mats, outs):
+            self._check_out(y, R, N)
+        for i in range(0, len(mats), 3):
+            ops.gemv_q8k_multi(mats[i:i + 3], xq, N, list(outs[i:i + 3]))
+        return 1
+
+    def rmsfold_q8k(self, h, w, residual=None, xn=None):
+        """h += residual (when given, in place), then RMSNorm(h) * w written as Q8_K into the engine
+        workspace (and to xn when given).  Returns (xn, xq) for gemv_q8."""
+        N = 1 if h.dim() == 1 else h.shape[0]
+        D = h.shape[-1]
+        if D > self.max_cols or N > self.max_rows:
+            raise ValueError("input %dx%d exceeds the engine workspace %dx%d" % (N, D, self.max_rows, self.max_cols))
+        return ops.rms_q8k(h, w, residual=residual, xn=xn, xq=self.xq[: N * (D // QK) * Q8K_BYTES].view(N, -1))
+
+    def swiglu_q8k(self, gate, up, y=None):
+        """silu(gate) * up written as Q8_K into the engine workspace (and to y when given).
+        Returns (y, xq) for gemv_q8."""
+        N = 1 if gate.dim() == 1 else gate.shape[0]
+        n = gate.shape[-1]
+        if n > self.max_cols or N > self.max_rows:
+            raise ValueError("input %dx%d exceeds the engine workspace %dx%d" % (N, n, self.max_rows, self.max_cols))
+        return ops.swiglu_q8k(gate, up, y=y, xq=self.xq[: N * (n // QK) * Q8K_BYTES].view(N, -1))
 
     def gemv_batch(self, names, X, outs):
         """Speculative-verify GEMV: X [N][C], N <= 16; out[n][r] bit-identical to gemv on row n."""

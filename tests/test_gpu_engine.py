@@ -93,3 +93,36 @@ def test_dequant_row_matches_oracle(layer, orc, dev):
         row = eng.dequant(name, R - 3)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(row.cpu().numpy(), orc.dequant_row(W, R, C, ty, R - 3))
+
+
+def test_engine_producers_feed_gemv(layer, orc, dev):
+    """rmsfold_q8k -> gemv_q8 (q/k/v) and swiglu_q8k -> gemv_q8 (down) give the same outputs, bit for
+    bit, as gemv on the producers' fp32 outputs (which quantizes them itself)."""
+    w, host = layer
+    eng = Engine(w, mode="q8k")
+    rng = np.random.default_rng(3)
+    h = torch.from_numpy(rng.standard_normal(4096).astype(np.float32)).to(dev)
+    res = torch.from_numpy(rng.standard_normal(4096).astype(np.float32)).to(dev)
+    wn = torch.from_numpy((1 + 0.1 * rng.standard_normal(4096)).astype(np.float32)).to(dev)
+    xn = torch.empty(4096, device=dev)
+    names = ["attn_q", "attn_k", "attn_v"]
+    outs = [torch.empty(R, device=dev) for _, R, _, _ in LAYER[:3]]
+    h0 = h.cpu().numpy().copy()
+    _, xq = eng.rmsfold_q8k(h, wn, residual=res, xn=xn)
+    assert eng.gemv_q8(names, xq, outs) == 1
+    ref = [torch.empty_like(o) for o in outs]
+    eng.gemv(names, xn, ref)
+    for a, b in zip(outs, ref):
+        assert torch.equal(a, b)
+    h_want, xn_want = orc.rms_norm(h0, wn.cpu().numpy(), res.cpu().numpy())
+    np.testing.assert_array_equal(h.cpu().numpy(), h_want[0])
+    np.testing.assert_array_equal(xn.cpu().numpy(), xn_want[0])
+    g = torch.from_numpy((rng.standard_normal(12288) * 2).astype(np.float32)).to(dev)
+    u = torch.from_numpy(rng.standard_normal(12288).astype(np.float32)).to(dev)
+    y = torch.empty(12288, device=dev)
+    out = torch.empty(4096, device=dev)
+    _, xq2 = eng.swiglu_q8k(g, u, y=y)
+    eng.gemv_q8(["ffn_down"], xq2, [out])
+    ref2 = torch.empty_like(out)
+    eng.gemv(["ffn_down"], y, [ref2])
+    assert torch.equal(out, ref2)

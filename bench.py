@@ -315,6 +315,40 @@ def producers_extra(torch, rn, layers, dev, steps=320):
     return out
 
 
+def head_extra(torch, rn, dev):
+    """Output head 151936x4096 Q6_K with the greedy pick: fused (kq_gemv_q8k_argmax) against the GEMV
+    followed by kq_argmax; two resident copies (1 GB) alternate so the cache does not serve them."""
+    from kq import ops, quantize as kqq
+    R, C_ = 151936, 4096
+    w0 = torch.from_numpy(kqq.synthetic_matrix(R, C_, 14, seed=999)).to(dev)
+    ws_w = [w0, w0.clone()]
+    x = torch.from_numpy(kqq.synthetic_activations(1, C_, seed=0)).to(dev)
+    xq = ops.q8k_quantize(x)
+    y = torch.empty(R, device=dev)
+    aws = ops.argmax_workspace(dev)
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    lib = rn.lib
+    p = lambda t: C.c_void_p(t.data_ptr())
+
+    def fused():
+        for w in ws_w:
+            rn.check(lib.kq_gemv_q8k_argmax(p(w), R, C_, 14, p(xq), p(y), p(aws), p(out), rn.stream()))
+
+    def separate():
+        for w in ws_w:
+            rn.gemv(w, R, C_, 14, xq, 1, y, rn.stream())
+            rn.check(lib.kq_argmax(p(y), R, p(aws), p(out), rn.stream()))
+
+    res = {}
+    for name, fn in (("fused_us", fused), ("gemv_then_argmax_us", separate)):
+        g = capture(torch, fn)
+        time_graphs(torch, [g] * 3)
+        res[name] = round(time_graphs(torch, [g] * 10) / 20 * 1e6, 2)
+    res["weight_GB/s_fused"] = round(wbytes(R, C_, 14) / (res["fused_us"] * 1e-6) / 1e9, 1)
+    del ws_w, w0
+    return res
+
+
 def gemm_extra(torch, rn, dev, timed=True):
     """Prefill GEMM: M in {512, 2048}; 12288x4096 Q4_K and 4096x12288 Q6_K (timed=False: two
     direct calls per shape, for counter runs)."""
@@ -471,6 +505,8 @@ def main():
         result["prefill_gemm"] = gemm_extra(torch, rn, dev)
         del layers
         torch.cuda.empty_cache()
+        log("bench: output head")
+        result["head"] = head_extra(torch, rn, dev)
         log("bench: full decode stream")
         result["decode_stream"] = decode_stream_extra(torch, rn, dev)
     if not a.no_cpu:

@@ -110,6 +110,28 @@ int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const in
                       int N, float* const* y, const int64_t* ldy, void* stream);
 
 /*
+ * Greedy pick over the logits: *out = index of the largest y[i] (i < n), the smallest index among
+ * equal largest values; NaN is never chosen and an input with no value above -1e30 gives 0.  The
+ * rule of k_argmax (scripts/kindi_q4/kindi/kindi.cu:637-661), launched after the head GEMV by
+ * Engine.head (engine.py:323-331).  One launch: workgroups reduce their share and the last one to
+ * finish reduces the partials.  ws: kq_argmax_workspace() bytes, 256-byte aligned, zero-filled
+ * before its first use (each call leaves it ready for the next); calls sharing a workspace must be
+ * ordered (same stream or synchronised).  out: one device int.
+ */
+size_t kq_argmax_workspace(void);
+int kq_argmax(const float* y, int n, void* ws, int* out, void* stream);
+
+/*
+ * Output head with the greedy pick fused: y = W xq for one Q8_K token (as kq_gemv_q8k, same bits)
+ * and *out = argmax(y) as kq_argmax, which the GEMV workgroups compute from the values they store
+ * when C <= 4096 (one column pass), saving the argmax launch and the logits read-back; for larger C
+ * a separate argmax launch follows.  Replaces gemv([head]) + k_argmax in Engine.head
+ * (engine.py:326-328).  ws and out as for kq_argmax.
+ */
+int kq_gemv_q8k_argmax(const void* w, int R, int C, int type, const void* xq, float* y, void* ws, int* out,
+                       void* stream);
+
+/*
  * Prefill GEMM: Y[m][r] for M >= 1 activation rows (row stride ldy), int8 products with int32
  * accumulation and the fp32 epilogue above.  Slot of the ternary engine's chunk GEMM
  * k_mm_g5q (chunk.cu:820) driven by chunk.feed (chunk.py:378); the Q4 engine itself prefills

@@ -23,7 +23,8 @@
  *     kept to show that the double evaluation and GGML's fp32 one agree to tolerance;
  *   - the producers of the GEMV inputs: RMSNorm with residual add (q4_rms, q4.cu:39-46,
  *     and the CPU engine's rmsfold, kcpu4.c:123-139) and SwiGLU (q4_silu, q4.cu:36-38;
- *     kcpu4.c:77, 292), with a binary32 exp built from IEEE single operations.
+ *     kcpu4.c:77, 292), with a binary32 exp built from IEEE single operations;
+ *   - the greedy pick over the logits, k_argmax (kindi.cu:637-661).
  *
  * Build: gcc -O2 -ffp-contract=off -fopenmp -shared -fPIC (oracle/Makefile).
  */
@@ -387,4 +388,31 @@ void kqo_swiglu(const float* g, const float* u, int64_t n, float* y) {
 
 void kqo_expf_n(const float* x, int64_t n, float* y) {
     for (int64_t i = 0; i < n; i++) y[i] = kqo_expf(x[i]);
+}
+
+/* ------------------------------------------------------------------ greedy pick */
+
+/* k_argmax (scripts/kindi_q4/kindi/kindi.cu:637-661): 1024 threads, thread t scans
+ * e = t, t+1024, ... keeping the first strictly larger value (start -1e30, index 0), then a
+ * halving tree that prefers the larger value and, on equal values, the smaller index. */
+int kqo_argmax(const float* y, int64_t n) {
+    float bval[1024];
+    int bidx[1024];
+    for (int t = 0; t < 1024; t++) {
+        float bv = -1e30f;
+        int bi = 0;
+        for (int64_t e = t; e < n; e += 1024) {
+            const float v = y[e];
+            if (v > bv) { bv = v; bi = (int)e; }
+        }
+        bval[t] = bv; bidx[t] = bi;
+    }
+    for (int st = 512; st > 0; st >>= 1)
+        for (int t = 0; t < st; t++) {
+            const int i2 = t + st;
+            if (bval[i2] > bval[t] || (bval[i2] == bval[t] && bidx[i2] < bidx[t])) {
+                bval[t] = bval[i2]; bidx[t] = bidx[i2];
+            }
+        }
+    return bidx[0];
 }

@@ -59,6 +59,8 @@ def lib():
         L.kqo_rms_norm.argtypes = [_PF, _PF, C.c_int, _PF, C.c_int, _PF, C.c_int]
         L.kqo_swiglu.argtypes = [_PF, _PF, C.c_int64, _PF]
         L.kqo_expf_n.argtypes = [_PF, C.c_int64, _PF]
+        L.kqo_argmax.argtypes = [_PF, C.c_int64]
+        L.kqo_argmax.restype = C.c_int
         _lib = L
     return _lib
 
@@ -214,3 +216,9 @@ def swiglu(g, u):
     y = np.empty_like(g)
     lib().kqo_swiglu(_p(g, _PF), _p(u, _PF), g.size, _p(y, _PF))
     return y
+
+
+def argmax(y):
+    """k_argmax's pick over y (kqo_argmax)."""
+    y = np.ascontiguousarray(y, np.float32).reshape(-1)
+    return int(lib().kqo_argmax(_p(y, _PF), y.size))

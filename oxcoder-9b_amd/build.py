@@ -20,8 +20,8 @@ OBJ = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["api.hip", "q8k_quantize.hip", "producers.hip", "gemv_q8k.hip", "gemv_mfma.hip", "gemv_f32.hip",
-               "gemm_q8k.hip"]
+HIP_SOURCES = ["api.hip", "q8k_quantize.hip", "producers.hip", "argmax.hip", "gemv_q8k.hip", "gemv_mfma.hip",
+               "gemv_f32.hip", "gemm_q8k.hip"]
 HIP_FLAGS = [
     "--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

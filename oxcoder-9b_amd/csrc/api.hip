@@ -139,6 +139,34 @@ int kq_swiglu_q8k(const float* gate, const float* up, int n, int N, int64_t ld, 
     return check_launch(fn);
 }
 
+size_t kq_argmax_workspace(void) { return argmax_workspace_bytes(); }
+
+static int check_argmax_ws(const void* ws, const int* out, const char* fn) {
+    KQ_TRY(check_ptr(ws, 256, "ws", fn));
+    return check_ptr(out, 4, "out", fn);
+}
+
+int kq_argmax(const float* y, int n, void* ws, int* out, void* stream) {
+    static const char* fn = "kq_argmax";
+    if (n <= 0) return fail(KQ_ERR_ARG, "%s: n=%d must be positive", fn, n);
+    KQ_TRY(check_ptr(y, 4, "y", fn));
+    KQ_TRY(check_argmax_ws(ws, out, fn));
+    launch_argmax(y, n, static_cast<uint8_t*>(ws), out, as_stream(stream));
+    return check_launch(fn);
+}
+
+int kq_gemv_q8k_argmax(const void* w, int R, int C, int type, const void* xq, float* y, void* ws, int* out,
+                       void* stream) {
+    static const char* fn = "kq_gemv_q8k_argmax";
+    KQ_TRY(check_matrix(w, R, C, type, fn));
+    KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    KQ_TRY(check_ptr(y, 4, "y", fn));
+    KQ_TRY(check_argmax_ws(ws, out, fn));
+    launch_gemv_q8k_argmax(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), y,
+                           static_cast<uint8_t*>(ws), out, as_stream(stream));
+    return check_launch(fn);
+}
+
 int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, float* y,
                 int64_t ldy, void* stream) {
     static const char* fn = "kq_gemv_q8k";

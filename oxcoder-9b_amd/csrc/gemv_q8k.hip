@@ -16,6 +16,7 @@
 #include "kq_device.h"
 #include "kq_internal.h"
 #include "q4_lanes.h"
+#include "argmax_block.h"
 
 #ifndef KQ_GEMV_WAVES_PER_CU
 #define KQ_GEMV_WAVES_PER_CU 8
@@ -279,9 +280,12 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
 // prefetching the next unit.  Each (unit, token, row) pass value goes to LDS; after one barrier
 // the workgroup merges them with the same pass tree as the sequential kernel and stores y.  With
 // one pass the value is stored directly.
-template <int TYPE, int NT, int RPW>
+// AMAX (one matrix, one token, one pass): the argmax of the outputs as well, into *aout
+// (argmax_block.h; aws is its workspace).
+template <int TYPE, int NT, int RPW, bool AMAX>
 __global__ void __launch_bounds__(256)
-k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units, int P, int kmax) {
+k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units, int P, int kmax,
+                 uint8_t* aws, int* aout) {
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     extern __shared__ float part[];                    // [stream][k][t][r][pass]
@@ -324,6 +328,7 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
         return mg.w[m] + tile * tile_bytes + r0 * BS + gc * col_bytes;
     };
 
+    ArgBest best = arg_init();                         // AMAX: this lane's best output (lane 0)
     if (u_begin < u_end) {
         Act<TYPE> act[NT];
 #pragma unroll
@@ -355,7 +360,11 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
                     const float v = block_value(fr, act[t], p);
                     const float pv = slot_tree_f32(valid ? v : 0.0f);
                     if (P == 1) {
-                        if (lane == 0) mg.y[m][t * mg.ldy[m] + row0 + r] = __fadd_rn(pv, 0.0f);
+                        if (lane == 0) {
+                            const float yv = __fadd_rn(pv, 0.0f);
+                            mg.y[m][t * mg.ldy[m] + row0 + r] = yv;
+                            if (AMAX) arg_take(best, yv, (int)(row0 + r));
+                        }
                     } else if (lane == 0) {
                         mypart[((k * NT + t) * RPW + r) * P + pass] = pv;
                     }
@@ -368,7 +377,10 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
         while (step(bufA, bufB) && step(bufB, bufA)) {
         }
     }
-    if (P == 1) return;
+    if (P == 1) {
+        if (AMAX) arg_grid_finish(arg_wave_reduce(best), aws, aout);
+        return;
+    }
 
     __syncthreads();
     for (int st = 0; st < K; st++) {
@@ -411,8 +423,9 @@ static int pick_rpw(int nt, int type) {
 #endif
 }
 
-template <int TYPE, int NT, int RPW>
-static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s) {
+template <int TYPE, int NT, int RPW, bool AMAX = false>
+static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s, uint8_t* aws = nullptr,
+                    int* aout = nullptr) {
     MatGroup mg = mg0;
     int total = 0;
     for (int i = 0; i < 3; i++) {
@@ -442,8 +455,8 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
                 nwg = round_xcd(nwg * 2);
             }
         }
-        hipLaunchKernelGGL((k_gemv_q8k_split<TYPE, NT, RPW>), dim3(nwg), dim3(64 * passes * K), lds, s, mg, xq, G,
-                           total, passes, kmax);
+        hipLaunchKernelGGL((k_gemv_q8k_split<TYPE, NT, RPW, AMAX>), dim3(nwg), dim3(64 * passes * K), lds, s, mg, xq,
+                           G, total, passes, kmax, aws, aout);
         return;
     }
     const int wpb = 4;
@@ -503,6 +516,28 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
         if (type == TYPE_Q4_K) launch1<TYPE_Q4_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q4_K), s);
         else launch1<TYPE_Q6_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q6_K), s);
     }
+}
+
+// One token, one matrix, and the argmax of y (output head + greedy pick).  With one column pass
+// (C <= 4096) the GEMV itself finds it; otherwise a separate argmax launch follows.
+void launch_gemv_q8k_argmax(const uint8_t* w, int R, int C, int type, const uint8_t* xq, float* y, uint8_t* aws,
+                            int* aout, hipStream_t s) {
+    const int G = C / QK;
+    if (G > 16) {
+        int64_t ldy = R;
+        launch_gemv_q8k_group(1, &w, &R, C, type, xq, 1, &y, &ldy, s);
+        launch_argmax(y, R, aws, aout, s);
+        return;
+    }
+    MatGroup mg{};
+    mg.n = 1;
+    mg.w[0] = w;
+    mg.y[0] = y;
+    mg.ldy[0] = R;
+    mg.first_unit[0] = 0;
+    for (int i = 1; i < 4; i++) mg.first_unit[i] = R / 8;
+    if (type == TYPE_Q4_K) launch3<TYPE_Q4_K, 1, 2, true>(mg, xq, G, s, aws, aout);
+    else launch3<TYPE_Q6_K, 1, 1, true>(mg, xq, G, s, aws, aout);
 }
 
 void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N, float* y,

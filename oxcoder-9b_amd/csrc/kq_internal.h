@@ -44,6 +44,12 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
 size_t gemm_q8k_workspace(int C, int M);
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
                      uint8_t* ws, hipStream_t s);
+// Argmax (argmax_block.h): ws holds argmax_workspace_bytes() bytes, its first word zero.
+size_t argmax_workspace_bytes();
+void launch_argmax(const float* y, int n, uint8_t* ws, int* out, hipStream_t s);
+// One-token GEMV of one matrix plus the argmax of its outputs.
+void launch_gemv_q8k_argmax(const uint8_t* w, int R, int C, int type, const uint8_t* xq, float* y, uint8_t* ws,
+                            int* out, hipStream_t s);
 void launch_subblock_sums(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N,
                           int32_t* sums, hipStream_t s);
 void launch_gemv_f32(const uint8_t* w, int R, int C, int type, const float* x, float* y,

@@ -20,6 +20,9 @@ KQ_SYMBOLS = {
     "kq_q8k_quantize": (_i, [_vp, _i64, _i, _i, _vp, _vp]),
     "kq_rms_q8k": (_i, [_vp, _vp, _i, _vp, _i, _i, _i64, _vp, _vp, _vp]),
     "kq_swiglu_q8k": (_i, [_vp, _vp, _i, _i, _i64, _vp, _vp, _vp]),
+    "kq_argmax_workspace": (C.c_size_t, []),
+    "kq_argmax": (_i, [_vp, _i, _vp, _vp, _vp]),
+    "kq_gemv_q8k_argmax": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "kq_gemv_q8k": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),
     "kq_gemv_q8k_multi": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, _i,
                                C.POINTER(_vp), C.POINTER(_i64), _vp]),

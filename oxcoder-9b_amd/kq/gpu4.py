@@ -19,7 +19,9 @@ same contract to several activation rows: X is [N][C] fp32, each out is [N][R] (
 The producers of the GEMV inputs write the Q8_K activation directly: ``rmsfold_q8k`` (the
 residual add + RMSNorm of Engine.rmsfold, gpu4.py:104-106 / q4_rms, q4.cu:39-46) and
 ``swiglu_q8k`` (q4_silu, q4.cu:36-38, as the FFN launches it, engine.py:287); ``gemv_q8`` then
-runs the named matrices on that Q8_K input with no further quantization.
+runs the named matrices on that Q8_K input with no further quantization.  ``head`` is the output
+head with the greedy pick (Engine.head, engine.py:323-331): the GEMV computes the argmax of the
+logits as it stores them (kq_gemv_q8k_argmax).
 """
 import torch
 
@@ -125,6 +127,25 @@ class Engine:
         if n > self.max_cols or N > self.max_rows:
             raise ValueError("input %dx%d exceeds the engine workspace %dx%d" % (N, n, self.max_rows, self.max_cols))
         return ops.swiglu_q8k(gate, up, y=y, xq=self.xq[: N * (n // QK) * Q8K_BYTES].view(N, -1))
+
+    def head(self, name, x, y=None):
+        """Greedy next token: y = W_name x (the logits, kept in ``y`` or the engine's buffer) and the
+        index of the largest logit, read back to the host as Engine.head does (engine.py:323-331,
+        gemv + k_argmax); the GEMV finds the argmax itself (kq_gemv_q8k_argmax)."""
+        w, R, C, ty = self.w[name]
+        if self.mode != "q8k":
+            raise ValueError("head: the fused greedy pick runs on Q8_K activations (mode 'q8k')")
+        if y is None:
+            if getattr(self, "logits", None) is None or self.logits.numel() < R:
+                self.logits = torch.empty(R, dtype=torch.float32, device=self.device)
+            y = self.logits[:R]
+        self._check_out(y, R)
+        if getattr(self, "argmax_ws", None) is None:
+            self.argmax_ws = ops.argmax_workspace(self.device)
+            self.argmax_out = torch.empty(1, dtype=torch.int32, device=self.device)
+        xq = self._quantize(x.reshape(1, -1)[:, :C], C)
+        ops.gemv_q8k_argmax(w, R, C, ty, xq, y, self.argmax_ws, self.argmax_out)
+        return int(self.argmax_out.cpu()[0])
 
     def gemv_batch(self, names, X, outs):
         """Speculative-verify GEMV: X [N][C], N <= 16; out[n][r] bit-identical to gemv on row n."""

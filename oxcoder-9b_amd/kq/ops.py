@@ -116,6 +116,37 @@ def swiglu_q8k(gate, up, y=None, xq=None):
     return y, xq
 
 
+def argmax_workspace(device):
+    """Zero-filled workspace for argmax / gemv_q8k_argmax (kq_argmax_workspace() bytes, 256-aligned)."""
+    n = int(_lib.kq().kq_argmax_workspace())
+    buf = torch.zeros(n + 256, dtype=torch.uint8, device=device)
+    off = (-buf.data_ptr()) % 256
+    return buf[off:off + n]
+
+
+def argmax(y, ws, out=None):
+    """Index of the largest y (k_argmax's rule) into out (device int32[1]); returns out."""
+    y = y.reshape(-1)
+    if y.stride(0) != 1:
+        raise ValueError("y must be contiguous")
+    out = torch.empty(1, dtype=torch.int32, device=y.device) if out is None else out
+    _lib.check(_lib.kq().kq_argmax(_dev(y, "y", torch.float32), y.numel(), _dev(ws, "ws", torch.uint8),
+                                   _dev(out, "out", torch.int32), _stream(y.device)))
+    return out
+
+
+def gemv_q8k_argmax(w, R, C_, ty, xq, y, ws, out=None):
+    """y = W xq (one Q8_K token) and out = argmax(y), fused (kq_gemv_q8k_argmax); returns out."""
+    pw = _weights(w, R, C_, ty)
+    if xq.numel() < (C_ // QK) * Q8K_BYTES or y.numel() < R:
+        raise ValueError("xq or y too small")
+    out = torch.empty(1, dtype=torch.int32, device=w.device) if out is None else out
+    _lib.check(_lib.kq().kq_gemv_q8k_argmax(pw, R, C_, ty, _dev(xq, "xq", torch.uint8), _dev(y, "y", torch.float32),
+                                            _dev(ws, "ws", torch.uint8), _dev(out, "out", torch.int32),
+                                            _stream(w.device)))
+    return out
+
+
 def gemv_q8k(w, R, C_, ty, xq, N, y, ldy=None):
     """Y[n][r] for N Q8_K activation rows (kq_gemv_q8k, N <= 16)."""
     pw = _weights(w, R, C_, ty)

@@ -126,3 +126,17 @@ def test_engine_producers_feed_gemv(layer, orc, dev):
     ref2 = torch.empty_like(out)
     eng.gemv(["ffn_down"], y, [ref2])
     assert torch.equal(out, ref2)
+
+
+def test_engine_head_greedy_pick(dev, orc):
+    """Engine.head -> int: the argmax of the logits (k_argmax's rule), logits left in y."""
+    R, C = 8192, 4096
+    w = Weights(dev)
+    W = kqq.synthetic_matrix(R, C, 14, seed=31)
+    w.add("output.weight", W, R, C, 14)
+    eng = Engine(w, mode="q8k")
+    x = torch.from_numpy(kqq.synthetic_activations(1, C, seed=2)[0]).to(dev)
+    y = torch.empty(R, device=dev)
+    tok = eng.head("output.weight", x, y)
+    assert tok == orc.argmax(y.cpu().numpy())
+    assert eng.head("output.weight", x) == tok            # engine-owned logits, workspace reused

@@ -187,3 +187,54 @@ def test_swiglu_check_rejects_planted_mistakes(mistake):
     with np.errstate(over="ignore"):
         assert swiglu_failures(py_swiglu()) == []
         assert swiglu_failures(py_swiglu(mistake)), mistake
+
+
+# ---------------------------------------------------------------------------------- greedy pick
+def argmax_failures(am):
+    """am(y) -> index.  The rule of k_argmax: largest value, smallest index among equals, NaN never
+    chosen, nothing above -1e30 -> 0."""
+    bad = []
+    rng = np.random.default_rng(8)
+    y = rng.standard_normal(151936).astype(F32)
+    if am(y) != int(np.argmax(y)):
+        bad.append("random")
+    t = y.copy()
+    t[[700, 90000, 150000]] = 9.0                         # three equal maxima
+    if am(t) != 700:
+        bad.append("ties")
+    t[5] = np.nan
+    t[6] = np.inf
+    if am(t) != 6:
+        bad.append("inf")
+    t[6] = 0.0
+    if am(t) != 700:
+        bad.append("nan")
+    if am(np.full(3000, -np.inf, F32)) != 0 or am(np.full(5, -2e30, F32)) != 0:
+        bad.append("nothing above -1e30")
+    neg = (-1 - rng.random(5000)).astype(F32)
+    if am(neg) != int(np.argmax(neg)):
+        bad.append("all negative")
+    if am(np.array([1.0], F32)) != 0 or am(np.array([-1e30, -1e29], F32)) != 1:
+        bad.append("small")
+    return bad
+
+
+def py_argmax(mistake=None):
+    def am(y):
+        y = np.asarray(y, F32)
+        bv, bi = (F32(0) if mistake == "start at 0" else F32(-1e30)), 0
+        for i, v in enumerate(y):
+            if (v >= bv) if mistake == "last max" else (v > bv or (mistake == "nan wins" and np.isnan(v))):
+                bv, bi = v, i
+        return bi
+    return am
+
+
+def test_argmax_rule(orc):
+    assert argmax_failures(orc.argmax) == []
+
+
+@pytest.mark.parametrize("mistake", ["start at 0", "last max", "nan wins"])
+def test_argmax_check_rejects_planted_mistakes(mistake):
+    assert argmax_failures(py_argmax()) == []
+    assert argmax_failures(py_argmax(mistake)), mistake

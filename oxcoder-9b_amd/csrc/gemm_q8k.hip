@@ -52,9 +52,6 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int GM_BMAX = 256;  // largest token tile: the fragment workspace is padded to it
 
-#ifndef KQ_GEMM_LO_VPM
-#define KQ_GEMM_LO_VPM 7  // VALU instructions placed after each MFMA of the second lo-sweep tile (epilogue of the first)
-#endif
 
 // Byte offset of 16-byte chunk `c` (0..15) of LDS plane row `r`: rows are 256 B, the chunk index
 // is XORed with the row's low 4 bits.
@@ -397,33 +394,24 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
             }
         };
 
-        // ---- lo sweep: acc = 2^SHIFT acc + A . L, one token tile after the other; the epilogue of
-        //      tile 0 runs under the MFMAs of tile 1, then this step's A fragments are replaced by
-        //      those of super-block g+1
-        v4i b[8];
+        // ---- lo sweep: acc = 2^SHIFT acc + A . L with both token tiles' accumulator chains
+        //      interleaved; each K step's A fragments are replaced by super-block g+1's right after
+        //      their last use; then both epilogues (the other wave of the SIMD keeps the MFMA pipe
+        //      busy meanwhile)
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) b[ks] = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0, 2 * ks + half));
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
+        for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int a = 0; a < 16; a++) acc[mt][a] <<= SHIFT;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-                acc[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[ks], acc[mt], 0, 0, 0);
+        for (int ks = 0; ks < 8; ks++) {
+            const v4i b = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0, 2 * ks + half));
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                acc[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b, acc[mt], 0, 0, 0);
+                afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
+            }
         }
         epilogue(0);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, KQ_GEMM_LO_VPM, 0);  // VALU (epilogue of tile 0)
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);             // DS read
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-                afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
         epilogue(1);
         __syncthreads();
     };

@@ -2,7 +2,9 @@
 
 ``Weights[name] -> (buf, R, C, type)`` mirrors gpu4.Weights.__getitem__ (gpu4.py:25-48): ``buf``
 is a device uint8 tensor in the Kindi 8-row layout, R/C/type int32 as in the pack index.  Here
-the tensors are registered in memory (device resident); reading a pack is not part of this path.
+the tensors are registered in memory (device resident); ``kq.pack.PackWeights`` gives the same
+contract over a Kindi pack on disk (verified as q4pack.verify_pack does), and either can back an
+Engine.
 
 ``Engine.gemv(names, x, outs, parts_ok=False) -> 1`` mirrors gpu4.Engine.gemv (gpu4.py:95-99):
 for each name, ``outs[i][:R] = W_name @ x`` on the current stream, asynchronously, returning 1
@@ -175,6 +177,14 @@ class Engine:
             self._check_out(y, R, M)
             ops.gemm_q8k(w, R, C_, ty, xq, M, y, y.stride(0), ws=self.gemm_ws)
         return 1
+
+    def embed(self, tok, out=None, name="token_embd.weight"):
+        """Row ``tok`` of the token embedding, decoded to fp32 (Engine.embed with q4_embed,
+        gpu4.py:100-103, q4.cu:28-32; kq_dequant_rows)."""
+        w, R, C, ty = self.w[name]
+        if not 0 <= tok < R:
+            raise ValueError("Invalid token")
+        return self.dequant(name, tok, out)
 
     def dequant(self, name, row, out=None):
         """One decoded row (kc_dequant, kcpu4.c:341; q4_embed, q4.cu:28-32)."""

@@ -1,0 +1,248 @@
+"""Kindi Q4 weight packs on the MI355X: verification, a device tensor cache, and a pack writer.
+
+A pack (scripts/kindi_q4/kindi/q4pack.py) is a directory with
+  weights.bin         quantized tensors in the 8-row interleave [R/8][G][8][bs], each starting at a
+                      16 KiB boundary and padded to one (q4pack.py:19, 151-160);
+  f32.bin             float tensors (norm weights, small gates), little-endian fp32;
+  index.json          {"tensors": {name: {rows, ne0, type, offset, bytes, padded_bytes} or
+                      {rows, ne0, type: 0, f32_off}}} (q4pack.py:145-160);
+  kindi_pack.json     manifest: pack_format "kindi-q4-v1", head, hadamard_block, dimensions,
+                      files {name: {size, sha256}} (q4pack.py:163-174).
+
+``verify_pack`` applies the reference's checks (q4pack.py:86-108) in the same order with the same
+messages.  ``PackWeights`` is the device side of gpu4.Weights (gpu4.py:17-48): ``w[name] ->
+(buf, R, C, type)`` with ``buf`` a device uint8 tensor in the Kindi layout, read with 8 MiB
+preads through two pinned staging buffers whose copies overlap the next read, a least-recently
+used byte budget that spares the embedding and the head, and POSIX_FADV_DONTNEED after each
+tensor so the host page cache does not keep a second copy.  On a 288 GB MI355X the default budget
+keeps the whole 9B pack (5.6 GB) resident.  ``write_pack`` builds a pack from tensors already in
+the Kindi layout (the converter from GGUF, q4pack.convert, is not part of this path).
+"""
+import hashlib
+import json
+import os
+from collections import OrderedDict
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from .formats import BLOCK
+
+PAGE = 16384
+PACK_FORMAT = "kindi-q4-v1"
+# Dimensions of the one validated profile (q4pack.py:79), the dense Qwen3.5 / OxCoder 9B.
+PROFILE_DIMS = {"layers": 32, "width": 4096, "ffn": 12288, "heads": 16, "kv_heads": 4, "head_dim": 256,
+                "rope_dim": 64, "groups": 16, "state_size": 128, "gdn_inner": 4096, "rope_base": 10000000.0,
+                "full_attention_interval": 4}
+PINNED = ("token_embd.weight", "output.weight")
+STAGE_BYTES = 8 << 20
+
+
+def profile_shapes(layers=32):
+    """name -> (rows, ne0) of the 9B profile (q4pack.py:21-35): every fourth layer (i % 4 == 3) is
+    full attention, the others gated delta-net; all layers have the FFN and two norms."""
+    shapes = {"output.weight": (248320, 4096), "token_embd.weight": (248320, 4096), "output_norm.weight": (1, 4096)}
+    for layer in range(layers):
+        p = "blk.%d." % layer
+        blk = {"attn_norm.weight": (1, 4096), "post_attention_norm.weight": (1, 4096),
+               "ffn_gate.weight": (12288, 4096), "ffn_up.weight": (12288, 4096), "ffn_down.weight": (4096, 12288)}
+        if layer % 4 == 3:
+            blk.update({"attn_q.weight": (8192, 4096), "attn_k.weight": (1024, 4096), "attn_v.weight": (1024, 4096),
+                        "attn_output.weight": (4096, 4096), "attn_q_norm.weight": (1, 256),
+                        "attn_k_norm.weight": (1, 256)})
+        else:
+            blk.update({"attn_qkv.weight": (8192, 4096), "attn_gate.weight": (4096, 4096),
+                        "ssm_out.weight": (4096, 4096), "ssm_alpha.weight": (32, 4096), "ssm_beta.weight": (32, 4096),
+                        "ssm_a": (1, 32), "ssm_dt.bias": (1, 32), "ssm_conv1d.weight": (8192, 4),
+                        "ssm_norm.weight": (1, 128)})
+        shapes.update({p + k: v for k, v in blk.items()})
+    return shapes
+
+
+def _float_storage(name, rows):
+    return rows == 1 or name.endswith(("ssm_alpha.weight", "ssm_beta.weight", "ssm_conv1d.weight"))
+
+
+def validate_shapes(index, shapes):
+    """q4pack.validate_shapes (q4pack.py:37-44) against the given profile."""
+    if set(index) != set(shapes):
+        raise ValueError("Missing/extra tensors for dense Qwen3.5 9B")
+    for name, (rows, cols) in shapes.items():
+        rec = index[name]
+        if (rec["rows"], rec["ne0"]) != (rows, cols):
+            raise ValueError("Unexpected shape: " + name)
+        if (rec["type"] == 0) != _float_storage(name, rows):
+            raise ValueError("Unexpected tensor storage: " + name)
+
+
+def digest(path):
+    h = hashlib.sha256()
+    with open(path, "rb") as f:
+        for b in iter(lambda: f.read(4 << 20), b""):
+            h.update(b)
+    return h.hexdigest()
+
+
+def verify_pack(pack, full=True, dims=PROFILE_DIMS, shapes=None):
+    """Checks of q4pack.verify_pack (q4pack.py:86-108); returns the manifest.  ``dims`` and
+    ``shapes`` default to the 9B profile."""
+    pack = Path(pack)
+    man = json.loads((pack / "kindi_pack.json").read_text())
+    if man["pack_format"] != PACK_FORMAT:
+        raise ValueError("Unsupported pack")
+    if man.get("dimensions") != dims or man.get("head") != "output.weight" or man.get("hadamard_block") != 1:
+        raise ValueError("Unsupported Q4 profile")
+    for name, rec in man["files"].items():
+        if Path(name).name != name:
+            raise ValueError("Invalid manifest path")
+        path = pack / name
+        if path.stat().st_size != rec["size"]:
+            raise ValueError("Pack size mismatch: " + name)
+        if full and digest(path) != rec["sha256"]:
+            raise ValueError("Pack checksum mismatch: " + name)
+    index = json.loads((pack / "index.json").read_text())["tensors"]
+    validate_shapes(index, profile_shapes() if shapes is None else shapes)
+    for rec in index.values():
+        if rec["type"] in BLOCK:
+            expected = rec["rows"] * (rec["ne0"] // 256) * BLOCK[rec["type"]]
+            if rec["rows"] % 8 or rec["ne0"] % 256 or expected != rec["bytes"]:
+                raise ValueError("Invalid packed tensor dimensions")
+            if (rec["offset"] < 0 or rec["offset"] % PAGE
+                    or rec["padded_bytes"] != (expected + PAGE - 1) // PAGE * PAGE
+                    or rec["offset"] + rec["padded_bytes"] > man["files"]["weights.bin"]["size"]):
+                raise ValueError("Invalid packed tensor span")
+        elif rec["type"] == 0:
+            if (rec["f32_off"] < 0 or rec["f32_off"] % 4
+                    or rec["f32_off"] + rec["rows"] * rec["ne0"] * 4 > man["files"]["f32.bin"]["size"]):
+                raise ValueError("Invalid float tensor span")
+        else:
+            raise ValueError("Invalid tensor type")
+    return man
+
+
+def write_pack(out, tensors, dims=PROFILE_DIMS, model="synthetic"):
+    """Write a pack.  tensors: name -> (data, rows, ne0, type); type 12/14: uint8 bytes already in
+    the Kindi layout; type 0: float32 values (rows x ne0).  Quantized tensors go to weights.bin at
+    16 KiB boundaries in the given order, floats to f32.bin.  Returns the manifest."""
+    out = Path(out)
+    out.mkdir(parents=True, exist_ok=False)
+    index = {}
+    with open(out / "weights.bin", "wb") as wb, open(out / "f32.bin", "wb") as fb:
+        for name, (data, rows, ne0, ty) in tensors.items():
+            rec = {"rows": int(rows), "ne0": int(ne0), "dims": [int(rows), int(ne0)], "type": int(ty), "folded": False}
+            if ty == 0:
+                a = np.ascontiguousarray(data, dtype="<f4").reshape(-1)
+                if a.size != rows * ne0:
+                    raise ValueError("float tensor %s has %d values, %dx%d expected" % (name, a.size, rows, ne0))
+                rec["f32_off"] = fb.tell()
+                fb.write(a.tobytes())
+            else:
+                a = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+                nbytes = rows * (ne0 // 256) * BLOCK[ty]
+                if a.size != nbytes:
+                    raise ValueError("tensor %s has %d bytes, %d expected" % (name, a.size, nbytes))
+                rec["offset"] = wb.tell()
+                rec["bytes"] = nbytes
+                rec["padded_bytes"] = (nbytes + PAGE - 1) // PAGE * PAGE
+                wb.write(a.tobytes())
+                wb.write(bytes(rec["padded_bytes"] - nbytes))
+            index[name] = rec
+    (out / "index.json").write_text(json.dumps({"tensors": index}, sort_keys=True))
+    man = {"pack_format": PACK_FORMAT, "model": model, "head": "output.weight", "hadamard_block": 1,
+           "dimensions": dims, "quantization": "mixed Q4_K/Q6_K; original blocks preserved",
+           "layout": "8-row-block-interleave",
+           "files": {p.name: {"size": p.stat().st_size, "sha256": digest(p)} for p in sorted(out.iterdir())}}
+    (out / "kindi_pack.json").write_text(json.dumps(man, indent=2) + "\n")
+    return man
+
+
+class PackWeights:
+    """Device tensor cache over a pack: ``w[name] -> (buf, R, C, type)`` (gpu4.py:25-48)."""
+
+    def __init__(self, pack, index=None, limit=None, device="cuda", pin_boundaries=True):
+        self.pack = Path(pack)
+        self.device = torch.device(device)
+        self.index = index if index is not None else json.loads((self.pack / "index.json").read_text())["tensors"]
+        self.fd = os.open(str(self.pack / "weights.bin"), os.O_RDONLY)
+        self.cache = OrderedDict()
+        self.used = self.read_bytes = self.hits = self.misses = 0
+        self.limit = int(limit) if limit is not None else 1 << 62
+        self.pin_boundaries = pin_boundaries
+        self._stage = None
+        self._f32 = {}
+
+    def close(self):
+        if self.fd is not None:
+            os.close(self.fd)
+            self.fd = None
+
+    def __del__(self):
+        self.close()
+
+    def __contains__(self, name):
+        return name in self.index and self.index[name]["type"] in BLOCK
+
+    def _staging(self):
+        if self._stage is None:
+            self._stage = [torch.empty(STAGE_BYTES, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+            self._events = [torch.cuda.Event(), torch.cuda.Event()]
+        return self._stage, self._events
+
+    def _evict_for(self, size):
+        protected = set(PINNED) if self.pin_boundaries else set()
+        while self.cache and self.used + size > self.limit:
+            key = next((k for k in self.cache if k not in protected), next(iter(self.cache)))
+            self.used -= self.cache[key][0].numel()
+            del self.cache[key]
+
+    def __getitem__(self, name):
+        if name in self.cache:
+            self.hits += 1
+            self.cache.move_to_end(name)
+            return self.cache[name]
+        self.misses += 1
+        rec = self.index[name]
+        if rec["type"] not in BLOCK:
+            raise ValueError("not a quantized tensor: " + name)
+        size = rec["bytes"]
+        self._evict_for(size)
+        buf = torch.empty(size, dtype=torch.uint8, device=self.device)
+        stage, events = self._staging()
+        stream = torch.cuda.current_stream(self.device)
+        for i, off in enumerate(range(0, size, STAGE_BYTES)):
+            n = min(STAGE_BYTES, size - off)
+            s, ev = stage[i % 2], events[i % 2]
+            ev.synchronize()                                   # its previous copy has finished
+            view = memoryview(s.numpy())[:n]
+            if os.preadv(self.fd, [view], rec["offset"] + off) != n:
+                raise IOError("Truncated Q4 weight tensor")
+            buf[off:off + n].copy_(s[:n], non_blocking=True)
+            ev.record(stream)
+            self.read_bytes += n
+        for ev in events:
+            ev.synchronize()
+        os.posix_fadvise(self.fd, rec["offset"], rec["padded_bytes"], os.POSIX_FADV_DONTNEED)
+        value = (buf, int(rec["rows"]), int(rec["ne0"]), int(rec["type"]))
+        self.cache[name] = value
+        self.used += size
+        return value
+
+    def f32(self, name):
+        """A float tensor of the pack (norm weights, gates) as a device fp32 tensor, kept."""
+        if name not in self._f32:
+            rec = self.index[name]
+            if rec["type"] != 0:
+                raise ValueError("not a float tensor: " + name)
+            n = rec["rows"] * rec["ne0"]
+            a = np.fromfile(self.pack / "f32.bin", dtype="<f4", count=n, offset=rec["f32_off"])
+            if a.size != n:
+                raise IOError("Truncated float tensor")
+            self._f32[name] = torch.from_numpy(a.astype(np.float32)).to(self.device)
+        return self._f32[name]
+
+
+def open_pack(pack, full=True, limit=None, device="cuda", dims=PROFILE_DIMS, shapes=None):
+    """verify_pack, then a PackWeights over the pack (the Engine's weights, gpu4.py:59)."""
+    verify_pack(pack, full=full, dims=dims, shapes=shapes)
+    return PackWeights(pack, limit=limit, device=device)

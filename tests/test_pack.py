@@ -1,0 +1,122 @@
+"""Kindi pack format on the host: writer, verify_pack's checks and messages (q4pack.py:86-108),
+and the 9B profile table (q4pack.py:21-35).  No GPU."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from kq import pack, quantize as kqq
+
+TINY_DIMS = {"layers": 1, "width": 256}
+TINY = {"token_embd.weight": (16, 256, 12), "output.weight": (16, 256, 14), "output_norm.weight": (1, 256, 0),
+        "blk.0.ffn_down.weight": (8, 512, 14), "blk.0.ssm_alpha.weight": (32, 256, 0)}
+
+
+def tiny_tensors():
+    out = {}
+    for i, (name, (R, C, ty)) in enumerate(TINY.items()):
+        data = (np.random.default_rng(i).standard_normal((R, C)).astype(np.float32) if ty == 0
+                else kqq.synthetic_matrix(R, C, ty, seed=i))
+        out[name] = (data, R, C, ty)
+    return out
+
+
+def tiny_shapes():
+    return {n: (R, C) for n, (R, C, _) in TINY.items()}
+
+
+@pytest.fixture
+def tiny_pack(tmp_path):
+    p = tmp_path / "pack"
+    pack.write_pack(p, tiny_tensors(), dims=TINY_DIMS)
+    return p
+
+
+def test_written_pack_verifies_and_is_aligned(tiny_pack):
+    man = pack.verify_pack(tiny_pack, full=True, dims=TINY_DIMS, shapes=tiny_shapes())
+    assert man["pack_format"] == "kindi-q4-v1" and man["head"] == "output.weight"
+    index = json.loads((tiny_pack / "index.json").read_text())["tensors"]
+    raw = np.fromfile(tiny_pack / "weights.bin", np.uint8)
+    for name, (data, R, C, ty) in tiny_tensors().items():
+        rec = index[name]
+        if ty == 0:
+            f = np.fromfile(tiny_pack / "f32.bin", "<f4", count=R * C, offset=rec["f32_off"])
+            np.testing.assert_array_equal(f, data.reshape(-1))
+        else:
+            assert rec["offset"] % pack.PAGE == 0 and rec["padded_bytes"] % pack.PAGE == 0
+            np.testing.assert_array_equal(raw[rec["offset"]:rec["offset"] + rec["bytes"]], data)
+
+
+def _rewrite_index(p, idx):
+    """Replace index.json and refresh its manifest record, so only the index content is wrong."""
+    f = p / "index.json"
+    f.write_text(json.dumps(idx))
+    man = json.loads((p / "kindi_pack.json").read_text())
+    man["files"]["index.json"] = {"size": f.stat().st_size, "sha256": pack.digest(f)}
+    (p / "kindi_pack.json").write_text(json.dumps(man))
+
+
+def _edit_index(p, name, **kv):
+    idx = json.loads((p / "index.json").read_text())
+    idx["tensors"][name].update(kv)
+    _rewrite_index(p, idx)
+
+
+@pytest.mark.parametrize("damage,msg", [
+    ("flip", "Pack checksum mismatch: weights.bin"),
+    ("truncate", "Pack size mismatch: weights.bin"),
+    ("format", "Unsupported pack"),
+    ("dims", "Unsupported Q4 profile"),
+    ("offset", "Invalid packed tensor span"),
+    ("bytes", "Invalid packed tensor dimensions"),
+    ("f32", "Invalid float tensor span"),
+    ("missing", "Missing/extra tensors"),
+    ("storage", "Unexpected tensor storage: blk.0.ssm_alpha.weight"),
+])
+def test_verify_pack_rejects_damage(tiny_pack, damage, msg):
+    p = tiny_pack
+    if damage == "flip":
+        with open(p / "weights.bin", "r+b") as f:
+            f.seek(100)
+            b = f.read(1)
+            f.seek(100)
+            f.write(bytes([b[0] ^ 1]))
+        pack.verify_pack(p, full=False, dims=TINY_DIMS, shapes=tiny_shapes())   # sizes still agree
+    elif damage == "truncate":
+        os.truncate(p / "weights.bin", os.path.getsize(p / "weights.bin") - 1)
+    elif damage in ("format", "dims"):
+        man = json.loads((p / "kindi_pack.json").read_text())
+        if damage == "format":
+            man["pack_format"] = "kindi-q4-v0"
+        else:
+            man["dimensions"] = {"layers": 2, "width": 256}
+        (p / "kindi_pack.json").write_text(json.dumps(man))
+    elif damage == "offset":
+        _edit_index(p, "output.weight", offset=4096)
+    elif damage == "bytes":
+        _edit_index(p, "output.weight", bytes=100)
+    elif damage == "f32":
+        _edit_index(p, "output_norm.weight", f32_off=2)
+    elif damage == "missing":
+        idx = json.loads((p / "index.json").read_text())
+        del idx["tensors"]["blk.0.ffn_down.weight"]
+        _rewrite_index(p, idx)
+    elif damage == "storage":
+        _edit_index(p, "blk.0.ssm_alpha.weight", type=12)
+    with pytest.raises(ValueError, match=msg):
+        pack.verify_pack(p, full=True, dims=TINY_DIMS, shapes=tiny_shapes())
+
+
+def test_profile_table_of_the_9b_model():
+    """427 tensors: 3 shared, 8 attention layers of 11 and 24 gated-delta-net layers of 14; the
+    float-stored ones are the norms, ssm_a/dt, conv1d and the alpha/beta gates."""
+    s = pack.profile_shapes()
+    assert len(s) == 3 + 8 * 11 + 24 * 14
+    assert s["blk.3.attn_q.weight"] == (8192, 4096) and "blk.3.attn_qkv.weight" not in s
+    assert s["blk.0.attn_qkv.weight"] == (8192, 4096) and s["blk.31.ffn_down.weight"] == (4096, 12288)
+    assert s["output.weight"] == (248320, 4096)
+    floats = [n for n, (r, _) in s.items() if pack._float_storage(n, r)]
+    assert len(floats) == 1 + 8 * 4 + 24 * 8
+    quant = {n: rc for n, rc in s.items() if not pack._float_storage(n, rc[0])}
+    assert all(r % 8 == 0 and c % 256 == 0 for r, c in quant.values())

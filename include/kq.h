@@ -44,6 +44,13 @@ const char* kq_last_error(void);
 int kq_version(void);
 
 /*
+ * Hash of the sources the library was built from (kernels, their headers, this file): a change of
+ * the arithmetic changes it.  For the engine's state-cache fingerprint, which keys saved states on
+ * the code of the arithmetic (engine_fingerprint and _ARITH, scripts/kindi_q4/kindi/cache.py:51-95).
+ */
+const char* kq_source_hash(void);
+
+/*
  * y[r] = sum_j w[r][j] * x[j] with fp32 activations: Kindi's decode GEMV.
  * Replaces the CUDA kernel q4_gemv(w, x, y, R, C, type) (scripts/kindi_q4/kindi/q4.cu:18-27) as
  * launched by Engine.gemv (gpu4.py:95-99), and kc_matvec (kcpu4.c:337-340).  Weights decode as

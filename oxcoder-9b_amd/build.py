@@ -8,6 +8,7 @@ kernels spells out each fused multiply-add explicitly) and with packed fp32 inst
 Run ``python oxcoder-9b_amd/build.py`` or call ``build()``.
 """
 import concurrent.futures as cf
+import hashlib
 import os
 import subprocess
 import sys
@@ -47,8 +48,22 @@ def _run(cmd):
         sys.stderr.write(rest + "\n")
 
 
+def source_hash():
+    """sha256 (first 16 hex digits) of every source that decides libkq's arithmetic: the kernels,
+    their headers and include/kq.h, in name order.  Compiled into the library (kq_source_hash) so
+    an engine can key saved states on the code that made them."""
+    h = hashlib.sha256()
+    files = sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".h")))
+    for f in files + ["../../include/kq.h"]:
+        path = os.path.normpath(os.path.join(CSRC, f))
+        h.update(os.path.basename(path).encode() + b"\0" + open(path, "rb").read())
+    return h.hexdigest()[:16]
+
+
 def _compile_hip(src):
     extra = HIP_EXTRA.get(src, [])
+    if src == "api.hip":
+        extra = extra + ['-DKQ_SOURCE_HASH="%s"' % source_hash()]
     obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
     _run([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj

@@ -70,6 +70,11 @@ const char* kq_last_error(void) { return g_err; }
 
 int kq_version(void) { return (1 << 16) | 0; }
 
+#ifndef KQ_SOURCE_HASH
+#define KQ_SOURCE_HASH "unknown"
+#endif
+const char* kq_source_hash(void) { return KQ_SOURCE_HASH; }
+
 int kq_gemv(const void* w, int R, int C, int type, const float* x, float* y, void* stream) {
     static const char* fn = "kq_gemv";
     KQ_TRY(check_matrix(w, R, C, type, fn));

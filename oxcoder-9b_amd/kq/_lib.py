@@ -15,6 +15,7 @@ _vp, _i, _i64 = C.c_void_p, C.c_int, C.c_int64
 KQ_SYMBOLS = {
     "kq_last_error": (C.c_char_p, []),
     "kq_version": (_i, []),
+    "kq_source_hash": (C.c_char_p, []),
     "kq_gemv": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "kq_gemv_multi": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, C.POINTER(_vp), _vp]),
     "kq_q8k_quantize": (_i, [_vp, _i64, _i, _i, _vp, _vp]),

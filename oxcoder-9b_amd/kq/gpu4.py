@@ -149,6 +149,24 @@ class Engine:
         ops.gemv_q8k_argmax(w, R, C, ty, xq, y, self.argmax_ws, self.argmax_out)
         return int(self.argmax_out.cpu()[0])
 
+    def feed_rows(self, names, X, outs, batch_max=16):
+        """Several activation rows through the named matrices, as the engine's batched prompt and
+        verify paths need (Runner batching, cache.py:587-600; chunk.feed, chunk.py:378): up to
+        ``batch_max`` rows go through the batched GEMV, whose rows are bit-identical to one-token
+        decode (so a verified draft continues exactly as decode would), more rows through the
+        prefill GEMM."""
+        N = X.shape[0]
+        if N <= batch_max:
+            return self.gemv_batch(names, X, outs)
+        return self.gemm(names, X, outs)
+
+    def fingerprint(self):
+        """Identity of this engine's arithmetic for a state cache (engine_fingerprint,
+        cache.py:55-95): the libkq source hash and the numerics mode."""
+        from . import _lib
+        return {"libkq": _lib.kq().kq_source_hash().decode(), "mode": self.mode,
+                "weights": "kindi-q4-v1: Q4_K/Q6_K row tiles"}
+
     def gemv_batch(self, names, X, outs):
         """Speculative-verify GEMV: X [N][C], N <= 16; out[n][r] bit-identical to gemv on row n."""
         N, C = X.shape

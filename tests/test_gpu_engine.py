@@ -140,3 +140,25 @@ def test_engine_head_greedy_pick(dev, orc):
     tok = eng.head("output.weight", x, y)
     assert tok == orc.argmax(y.cpu().numpy())
     assert eng.head("output.weight", x) == tok            # engine-owned logits, workspace reused
+
+
+def test_engine_feed_rows_dispatch(layer, dev):
+    """feed_rows: up to 16 rows through the batched GEMV (rows equal one-token decode bit for bit),
+    more through the GEMM (same values within the GEMM's own bar, bit-equal to Engine.gemm)."""
+    w, host = layer
+    eng = Engine(w, mode="q8k", max_rows=64)
+    X = torch.from_numpy(kqq.synthetic_activations(40, 4096, seed=9)).to(dev)
+    names = ["ffn_gate"]
+    y5 = torch.empty((5, 12288), device=dev)
+    eng.feed_rows(names, X[:5], [y5])
+    for n in range(5):
+        one = torch.empty(12288, device=dev)
+        eng.gemv(names, X[n], [one])
+        assert torch.equal(y5[n], one)
+    y40 = torch.empty((40, 12288), device=dev)
+    eng.feed_rows(names, X, [y40])
+    ref = torch.empty_like(y40)
+    eng.gemm(names, X, [ref])
+    assert torch.equal(y40, ref)
+    fp = eng.fingerprint()
+    assert len(fp["libkq"]) == 16 and fp["mode"] == "q8k"

@@ -136,3 +136,14 @@ def test_producer_argument_errors():
     assert rc == _lib.KQ_ERR_ARG and "N=0" in lib.kq_last_error().decode()
     rc = lib.kq_swiglu_q8k(p, None, 256, 1, 256, None, p, None)
     assert rc == _lib.KQ_ERR_ARG and "up is NULL" in lib.kq_last_error().decode()
+
+
+def test_source_hash_is_the_built_sources():
+    """kq_source_hash names the sources the loaded library was built from."""
+    import importlib.util
+    from kq import _lib
+    spec = importlib.util.spec_from_file_location("kq_build", os.path.join(ROOT, "oxcoder-9b_amd", "build.py"))
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    h = _lib.kq().kq_source_hash().decode()
+    assert len(h) == 16 and h == b.source_hash()

@@ -13,6 +13,8 @@
 // bytes plus scales and d with dword-aligned funnel-shifted loads.  Per (row, super-block) the
 // four lanes' int32 partials are summed exactly, turned into one fp32 value and reduced by the
 // column tree of q4_lanes.h, so the result does not depend on NT, RPW or grid shape.
+#include <type_traits>
+
 #include "kq_device.h"
 #include "kq_internal.h"
 #include "q4_lanes.h"
@@ -38,6 +40,9 @@
 #endif
 #ifndef KQ_GEMV_BLOCKED
 #define KQ_GEMV_BLOCKED 0  // 1: contiguous unit ranges per stream, streams grouped per XCD
+#endif
+#ifndef KQ_GEMV_P3
+#define KQ_GEMV_P3 1       // three-pass matrices (C = 8448..12288) keep every pass's activations in registers
 #endif
 #ifndef KQ_XCDS
 #define KQ_XCDS 8          // accelerator complex dies per MI355X; workgroups alternate between them
@@ -169,7 +174,10 @@ __device__ __forceinline__ float block_value(const Q6Fields& f, const Act<TYPE_Q
 }
 
 // ------------------------------------------------------------------ the kernel
-template <int TYPE, int NT, int RPW, bool ONEPASS>
+// FP = 3: exactly three column passes (C = 8448 .. 12288, the FFN down projection), with the
+// activations of all three held in registers instead of reloaded at every (unit, pass) step;
+// the step loop is unrolled over the passes so each step's pass is a compile-time index.
+template <int TYPE, int NT, int RPW, bool ONEPASS, int FP = 0>
 __global__ void __launch_bounds__(256)
 k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) {
     constexpr int WPT = 8 / RPW;
@@ -180,7 +188,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
     int u = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (u >= total_units) return;
     const int p = lane & 3, slot = lane >> 2;
-    const int passes = ONEPASS ? 1 : (G + 15) >> 4;
+    const int passes = ONEPASS ? 1 : FP ? FP : (G + 15) >> 4;
     const int64_t col_bytes = 8 * BS;                  // one tile column
     const int64_t tile_bytes = (int64_t)G * col_bytes;
 
@@ -203,6 +211,15 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
     if (ONEPASS) {
 #pragma unroll
         for (int t = 0; t < NT; t++) load_act(act[t], XQ + ((int64_t)t * G + slot_c) * Q8K_BYTES, p);
+    }
+    Act<TYPE> actp[FP ? FP : 1][NT];                   // FP: every pass's activations
+    if (FP) {
+#pragma unroll
+        for (int q = 0; q < (FP ? FP : 1); q++) {
+            const int gq = slot + 16 * q < G ? slot + 16 * q : G - 1;
+#pragma unroll
+            for (int t = 0; t < NT; t++) load_act(actp[q][t], XQ + ((int64_t)t * G + gq) * Q8K_BYTES, p);
+        }
     }
 
     Frag<TYPE> bufA[RPW], bufB[RPW];
@@ -269,7 +286,57 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
         u = un; pass = pn; m = mn; row0 = row0n; base = basen;
         return true;
     };
-    while (step(bufA, bufB) && step(bufB, bufA)) {
+    if constexpr (FP == 3) {
+        // step with a compile-time pass PS: the same work as `step`, activations from registers
+        auto stepf = [&](auto pass_c, Frag<TYPE>* cur, Frag<TYPE>* nxt) -> bool {
+            constexpr int PS = decltype(pass_c)::value;
+            constexpr int PN = PS + 1 == FP ? 0 : PS + 1;
+            const int un = PN == 0 ? u + nwaves : u;
+            const bool has_next = un < total_units;
+            int mn = m;
+            int64_t row0n = row0;
+            const uint8_t* basen = base;
+            if (has_next && PN == 0) basen = unit_base(un, mn, row0n);
+            {
+                int gn = slot + 16 * (has_next ? PN : PS);
+                gn = gn < G ? gn : G - 1;
+#pragma unroll
+                for (int r = 0; r < RPW; r++) load_frag(nxt[r], basen + (int64_t)gn * col_bytes + r * BS, p);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const bool valid = slot + 16 * PS < G;
+#pragma unroll
+            for (int r = 0; r < RPW; r++) {
+                const auto fr = prepare(cur[r], p);
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const float v = block_value(fr, actp[PS][t], p);
+                    tree_push(tree[t][r], slot_tree_f32(valid ? v : 0.0f));
+                }
+            }
+            if (PS == FP - 1) {
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+#pragma unroll
+                    for (int r = 0; r < RPW; r++) {
+                        const float y = tree_final(tree[t][r]);
+                        if (lane == 0) mg.y[m][t * mg.ldy[m] + row0 + r] = y;
+                        tree_init(tree[t][r]);
+                    }
+            }
+            if (!has_next) return false;
+            u = un; m = mn; row0 = row0n; base = basen;
+            return true;
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        while (stepf(I0{}, bufA, bufB) && stepf(I1{}, bufB, bufA) && stepf(I2{}, bufA, bufB) &&
+               stepf(I0{}, bufB, bufA) && stepf(I1{}, bufA, bufB) && stepf(I2{}, bufB, bufA)) {
+        }
+    } else {
+        while (step(bufA, bufB) && step(bufB, bufA)) {
+        }
     }
 }
 
@@ -463,6 +530,12 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
     int waves = device_cus() * wpc;
     if (waves > total) waves = total;
     dim3 grid((waves + wpb - 1) / wpb), block(64 * wpb);
+    if constexpr (KQ_GEMV_P3 && NT <= 2 && RPW <= 2) {
+        if (passes == 3) {
+            hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false, 3>), grid, block, 0, s, mg, xq, G, total);
+            return;
+        }
+    }
     if (G <= 16)
         hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, true>), grid, block, 0, s, mg, xq, G, total);
     else

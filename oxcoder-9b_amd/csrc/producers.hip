@@ -48,15 +48,21 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, kq_expf(-g))), u);
 }
 
-// One workgroup of 256 threads per row; J >= D/256 row elements per thread (a compile-time count,
-// so every load is unconditional: elements past D re-read element D-1 and are not used).  Every
-// global load of the row (h, residual, and the w values of pass 2) is issued up front, so the
-// kernel waits for memory once.  Dynamic LDS holds the row (D floats) between the two passes.
+// One workgroup of 1024 (or 512) threads per row.  Threads 0..255 do the first pass (J >= D/256 row
+// elements each, a compile-time count, so every load is unconditional: elements past D re-read
+// element D-1 and are not used); all 16 waves then quantize, each one 256-value block in turn
+// (D/256 blocks), so the blocks' dependent cross-lane steps run side by side instead of one
+// after another in four waves.  Every global load
+// of the row (h, residual, and the w values of pass 2) is issued up front, so the kernel waits for
+// memory once.  Dynamic LDS holds the row (D floats) between the two passes.
+// (8 waves when J > 32: 16 would leave 128 VGPRs per thread for the J row values and spill.)
+template <int J> constexpr int rms_waves() { return J <= 32 ? 16 : 8; }
 template <int J>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * rms_waves<J>())
 k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int D, int64_t ld, float* xn,
           uint8_t* __restrict__ xq) {
-    constexpr int B = (J + 3) / 4;             // Q8_K blocks per wave, at most
+    constexpr int RMS_WAVES = rms_waves<J>();
+    constexpr int B = (J + RMS_WAVES - 1) / RMS_WAVES;   // Q8_K blocks per wave, at most
     extern __shared__ float hrow[];            // D floats
     __shared__ double sums[128];
     __shared__ float s_sh;
@@ -65,37 +71,42 @@ k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int 
     const int G = D / QK;
     float* hr = h + (int64_t)row * ld;
     const float* rr = res + (int64_t)row * ld;
+    const bool first = t < 256;                // a thread of the first pass
     auto at = [&](int k) { const int i = t + 256 * k; return i < D ? i : D - 1; };
 
     float v[J];
+    if (first) {
 #pragma unroll
-    for (int k = 0; k < J; k++) v[k] = hr[at(k)];
-    if (add) {
-        float r[J];
+        for (int k = 0; k < J; k++) v[k] = hr[at(k)];
+        if (add) {
+            float r[J];
 #pragma unroll
-        for (int k = 0; k < J; k++) r[k] = rr[at(k)];
+            for (int k = 0; k < J; k++) r[k] = rr[at(k)];
 #pragma unroll
-        for (int k = 0; k < J; k++) v[k] = __fadd_rn(v[k], r[k]);
+            for (int k = 0; k < J; k++) v[k] = __fadd_rn(v[k], r[k]);
+        }
     }
-    f32x4 wq[B];                               // pass 2 operands: w of blocks wv, wv + 4, ...
+    f32x4 wq[B];                               // pass 2 operands: w of blocks wv, wv + 16, ...
 #pragma unroll
     for (int b = 0; b < B; b++) {
-        const int g = wv + 4 * b < G ? wv + 4 * b : G - 1;
+        const int g = wv + RMS_WAVES * b < G ? wv + RMS_WAVES * b : G - 1;
         wq[b] = *reinterpret_cast<const f32x4_a4*>(w + g * QK + 4 * lane);
     }
 
-    // pass 1: thread t's partial sum over i = t, t + 256, ... in sequence (q4.cu:41)
+    // pass 1: thread t's partial sum over i = t, t + 256, ... in sequence (q4.cu:41).  The updated
+    // h goes to LDS now and to memory at the end, so no barrier below waits for global stores.
     double sum = 0.0;
+    if (first) {
 #pragma unroll
-    for (int k = 0; k < J; k++) {
-        if (t + 256 * k < D) {
-            if (add) hr[t + 256 * k] = v[k];
-            hrow[t + 256 * k] = v[k];
-            sum = __dadd_rn(sum, __dmul_rn((double)v[k], (double)v[k]));
+        for (int k = 0; k < J; k++) {
+            if (t + 256 * k < D) {
+                hrow[t + 256 * k] = v[k];
+                sum = __dadd_rn(sum, __dmul_rn((double)v[k], (double)v[k]));
+            }
         }
     }
     // the halving tree of q4.cu:42-43: sums[t] += sums[t + n] for n = 128, 64, ..., 1
-    if (t >= 128) sums[t - 128] = sum;
+    if (t >= 128 && t < 256) sums[t - 128] = sum;
     __syncthreads();
     if (t < 128) sum = __dadd_rn(sum, sums[t]);                 // n = 128
     __syncthreads();
@@ -115,12 +126,12 @@ k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int 
     __syncthreads();
     const float s = s_sh;
 
-    // pass 2: Q8_K blocks; wave wv takes blocks wv, wv + 4, ...; lane l the values 4l .. 4l+3.
-    // xn may be h itself: the values now come from LDS.
+    // pass 2: Q8_K blocks; wave wv takes blocks wv, wv + 16, ...; lane l the values 4l .. 4l+3.
+    // xn may be h itself: the values come from LDS.
     float* xr = xn ? xn + (int64_t)row * ld : nullptr;
 #pragma unroll
     for (int b = 0; b < B; b++) {
-        const int g = wv + 4 * b;
+        const int g = wv + RMS_WAVES * b;
         if (g >= G) break;
         const int i0 = g * QK + 4 * lane;
         const f32x4 hv = *reinterpret_cast<const f32x4*>(hrow + i0);
@@ -131,6 +142,13 @@ k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int 
         e[3] = __fmul_rn(__fmul_rn(hv.w, s), wq[b].w);
         if (xr) *reinterpret_cast<f32x4_a4*>(xr + i0) = f32x4{e[0], e[1], e[2], e[3]};
         q8k_block_store(e, lane, xq + ((int64_t)row * G + g) * Q8K_BYTES);
+    }
+    // h += residual, written back; when xn is h itself the normalised values written above are
+    // the row's final contents (as when q4_rms writes h and then xn over it)
+    if (first && add && xn != h) {
+#pragma unroll
+        for (int k = 0; k < J; k++)
+            if (t + 256 * k < D) hr[t + 256 * k] = v[k];
     }
 }
 
@@ -158,14 +176,17 @@ void launch_rms_q8k(float* h, const float* res, int add, const float* w, int D, 
                     uint8_t* xq, hipStream_t s) {
     const size_t lds = (size_t)D * sizeof(float);
     const int j = (D + 255) / 256;             // row elements per thread: 1 .. 64 (D <= 16384)
-    const dim3 grid(N), block(256);
+    const dim3 grid(N);
     const float* r = res ? res : h;
-    if (j <= 4) hipLaunchKernelGGL(k_rms_q8k<4>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
-    else if (j <= 8) hipLaunchKernelGGL(k_rms_q8k<8>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
-    else if (j <= 16) hipLaunchKernelGGL(k_rms_q8k<16>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
-    else if (j <= 32) hipLaunchKernelGGL(k_rms_q8k<32>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
-    else if (j <= 48) hipLaunchKernelGGL(k_rms_q8k<48>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
-    else hipLaunchKernelGGL(k_rms_q8k<64>, grid, block, lds, s, h, r, add, w, D, ld, xn, xq);
+#define KQ_RMS_LAUNCH(JJ) \
+    hipLaunchKernelGGL(k_rms_q8k<JJ>, grid, dim3(64 * rms_waves<JJ>()), lds, s, h, r, add, w, D, ld, xn, xq)
+    if (j <= 4) KQ_RMS_LAUNCH(4);
+    else if (j <= 8) KQ_RMS_LAUNCH(8);
+    else if (j <= 16) KQ_RMS_LAUNCH(16);
+    else if (j <= 32) KQ_RMS_LAUNCH(32);
+    else if (j <= 48) KQ_RMS_LAUNCH(48);
+    else KQ_RMS_LAUNCH(64);
+#undef KQ_RMS_LAUNCH
 }
 
 void launch_swiglu_q8k(const float* gate, const float* up, int n, int N, int64_t ld, float* y, uint8_t* xq,

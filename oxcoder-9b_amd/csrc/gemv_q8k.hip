@@ -26,6 +26,16 @@
 #ifndef KQ_GEMV_WAVES_PER_CU_Q6
 #define KQ_GEMV_WAVES_PER_CU_Q6 KQ_GEMV_WAVES_PER_CU
 #endif
+// Q6_K on the sequential kernel: one workgroup of 4 waves per CU, one wave per SIMD, each wave
+// walking more units (4096x12288 at one token: 4 units per wave, 10.9 us against 11.6 us at 8
+// waves per CU; two tokens 12.8 against 13.9 us; 2, 3, 5 or 6 waves per CU and workgroups of 1
+// or 2 waves were slower).
+#ifndef KQ_GEMV_WAVES_PER_CU_SEQ_Q6
+#define KQ_GEMV_WAVES_PER_CU_SEQ_Q6 4
+#endif
+#ifndef KQ_GEMV_SEQ_WPB
+#define KQ_GEMV_SEQ_WPB 4        // waves per workgroup of the sequential kernel
+#endif
 #ifndef KQ_GEMV_MFMA_MIN_N
 #define KQ_GEMV_MFMA_MIN_N 3     // tokens per call from which the MFMA form (gemv_mfma.hip) is used
 #endif
@@ -526,8 +536,8 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
                            G, total, passes, kmax, aws, aout);
         return;
     }
-    const int wpb = 4;
-    int waves = device_cus() * wpc;
+    const int wpb = KQ_GEMV_SEQ_WPB;
+    int waves = device_cus() * (TYPE == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_SEQ_Q6 : wpc);
     if (waves > total) waves = total;
     dim3 grid((waves + wpb - 1) / wpb), block(64 * wpb);
     if constexpr (KQ_GEMV_P3 && NT <= 2 && RPW <= 2) {

@@ -20,6 +20,7 @@ import ctypes as C
 import json
 import os
 import sys
+import statistics
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -208,14 +209,15 @@ def traffic_from_profile(path=os.path.join(ROOT, "profiles", "gemv_q4k_decode_la
     return None
 
 
-def cpu_baseline(budget_s=12.0):
-    """The reference's CPU path (kc_matvec, fp32 activations) on the same layer shapes."""
+def cpu_baseline(budget_s=12.0, budget_2t_s=6.0, runs=5):
+    """The reference's CPU path (kc_matvec, fp32 activations) on the same layer shapes: `runs` timed
+    runs after one warm-up, median, at the box's CPU share (16 threads unless KQ_CPU_THREADS or
+    OMP_NUM_THREADS says otherwise) and at 2 threads (the reference's validated default,
+    scripts/kindi_q4/kindi/cpu4.py:99)."""
     from kq import quantize as kqq
     from oracle import oracle
     threads = int(os.environ.get("KQ_CPU_THREADS", os.environ.get("OMP_NUM_THREADS", "16")))
-    # libgomp has already read OMP_NUM_THREADS (the host quantizer uses it); set the team size
-    # of this thread's parallel regions through the runtime instead.
-    C.CDLL("libgomp.so.1").omp_set_num_threads(threads)
+    gomp = C.CDLL("libgomp.so.1")
     kind = "reference" if oracle.ref_available() else "port"
     mats = []
     for i, (name, R, C_, ty, slot) in enumerate(LAYER):
@@ -224,20 +226,37 @@ def cpu_baseline(budget_s=12.0):
     copies = [mats] + [[(W.copy(), R, C_, ty, x) for (W, R, C_, ty, x) in mats] for _ in range(3)]
     fn = oracle.ref_matvec if kind == "reference" else oracle.matvec_f32
     per_step = sum(wbytes(R, C_, ty) + C_ * 4 + R * 4 for (_, R, C_, ty, _) in mats)
-    for (W, R, C_, ty, x) in copies[0]:
-        fn(W, R, C_, ty, x)           # warm-up
-    t0 = time.perf_counter()
-    n = 0
-    while True:
-        for (W, R, C_, ty, x) in copies[n % len(copies)]:
-            fn(W, R, C_, ty, x)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(per_step * n / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": "%d decode-layer steps (7 matvecs, fp32 activations, kc_matvec%s) rotating 4 "
-                      "host copies (486 MB), %.1f s" % (n, "" if kind == "reference" else " restated", el)}
+
+    def timed(nthreads, seconds):
+        # libgomp has already read OMP_NUM_THREADS (the host quantizer uses it); set the team size
+        # of this thread's parallel regions through the runtime instead.
+        gomp.omp_set_num_threads(nthreads)
+        for (W, R, C_, ty, x) in copies[0]:
+            fn(W, R, C_, ty, x)           # warm-up
+        rates, steps = [], 0
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            n = 0
+            while True:
+                for (W, R, C_, ty, x) in copies[n % len(copies)]:
+                    fn(W, R, C_, ty, x)
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= seconds / runs:
+                    break
+            rates.append(per_step * n / el / 1e9)
+            steps += n
+        return statistics.median(rates), steps
+
+    v, n = timed(threads, budget_s)
+    v2, n2 = timed(2, budget_2t_s)
+    gomp.omp_set_num_threads(threads)
+    return {"value": round(v, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "value_2_threads": round(v2, 3),
+            "sample": "median of %d runs (%d decode-layer steps in %.0f s) of the 7 matvecs of one decode layer "
+                      "(fp32 activations, kc_matvec%s) rotating 4 host copies (486 MB); value_2_threads: the same, "
+                      "2 threads, %d steps in %.0f s" % (runs, n, budget_s, "" if kind == "reference" else " restated",
+                                                        n2, budget_2t_s)}
 
 
 def batched_extra(torch, rn, dev, steps):

@@ -48,14 +48,14 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, kq_expf(-g))), u);
 }
 
-// One workgroup of 1024 (or 512) threads per row.  Threads 0..255 do the first pass (J >= D/256 row
-// elements each, a compile-time count, so every load is unconditional: elements past D re-read
-// element D-1 and are not used); all 16 waves then quantize, each one 256-value block in turn
-// (D/256 blocks), so the blocks' dependent cross-lane steps run side by side instead of one
-// after another in four waves.  Every global load
-// of the row (h, residual, and the w values of pass 2) is issued up front, so the kernel waits for
-// memory once.  Dynamic LDS holds the row (D floats) between the two passes.
-// (8 waves when J > 32: 16 would leave 128 VGPRs per thread for the J row values and spill.)
+// One workgroup per row: 16 waves, or 8 when J > 32 (16 would leave 128 VGPRs per thread for the J
+// row values and spill).  Threads 0..255 do the first pass (J >= D/256 row elements each, a
+// compile-time count, so every load is unconditional: elements past D re-read element D-1 and are
+// not used); every wave then quantizes 256-value blocks (D/256 of them, one per wave up to
+// D = 4096), so the blocks' dependent cross-lane steps run side by side instead of one after
+// another in a few waves.  Every global load of the row (h, residual, and the w values of pass 2)
+// is issued up front, so the kernel waits for memory once.  Dynamic LDS holds the row (D floats)
+// between the two passes.
 template <int J> constexpr int rms_waves() { return J <= 32 ? 16 : 8; }
 template <int J>
 __global__ void __launch_bounds__(64 * rms_waves<J>())
@@ -86,7 +86,7 @@ k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int 
             for (int k = 0; k < J; k++) v[k] = __fadd_rn(v[k], r[k]);
         }
     }
-    f32x4 wq[B];                               // pass 2 operands: w of blocks wv, wv + 16, ...
+    f32x4 wq[B];                               // pass 2 operands: w of blocks wv, wv + RMS_WAVES, ...
 #pragma unroll
     for (int b = 0; b < B; b++) {
         const int g = wv + RMS_WAVES * b < G ? wv + RMS_WAVES * b : G - 1;
@@ -126,7 +126,7 @@ k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int 
     __syncthreads();
     const float s = s_sh;
 
-    // pass 2: Q8_K blocks; wave wv takes blocks wv, wv + 16, ...; lane l the values 4l .. 4l+3.
+    // pass 2: Q8_K blocks; wave wv takes blocks wv, wv + RMS_WAVES, ...; lane l the values 4l .. 4l+3.
     // xn may be h itself: the values come from LDS.
     float* xr = xn ? xn + (int64_t)row * ld : nullptr;
 #pragma unroll

@@ -31,7 +31,10 @@ def rms_inputs(N, D, seed):
     return h, r, w
 
 
-@pytest.mark.parametrize("N,D", [(1, 256), (1, 4096), (3, 4096), (2, 12288), (5, 768)])
+# D covers every row-length instantiation of the kernel: 768 (4 values per thread), 2560 (16), 4096
+# (16), 8192 (32, the last with 16 waves), 12288 (48, 8 waves), 16384 (64, the largest D)
+@pytest.mark.parametrize("N,D", [(1, 256), (1, 4096), (3, 4096), (2, 12288), (5, 768), (1, 2560), (2, 8192),
+                                 (1, 16384)])
 @pytest.mark.parametrize("add", [False, True])
 def test_rms_q8k_bit_exact(dev, orc, N, D, add):
     h, r, w = rms_inputs(N, D, seed=D + N)

@@ -379,7 +379,7 @@ def gemm_extra(torch, rn, dev, timed=True):
             X = torch.from_numpy(kqq.synthetic_activations(M, C_, seed=M)).to(dev)
             xq = ops.q8k_quantize(X)
             y = torch.empty((M, R), device=dev)
-            ws = torch.empty(ops.gemm_workspace_bytes(C_, M), dtype=torch.uint8, device=dev)
+            ws = ops.gemm_workspace(R, C_, M, dev)
             if not timed:
                 for _ in range(2):
                     rn.gemm(w, R, C_, ty, xq, M, y, ws, rn.stream())

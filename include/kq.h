@@ -147,15 +147,20 @@ int kq_gemv_q8k_argmax(const void* w, int R, int C, int type, const void* xq, fl
 int kq_gemm_q8k(const void* w, int R, int C, int type, const void* xq, int M, float* y,
                 int64_t ldy, void* stream);
 
-/* Bytes of device workspace kq_gemm_q8k_ws needs for M activation rows of C columns. */
-size_t kq_gemm_q8k_workspace(int C, int M);
+/* Bytes of device workspace kq_gemm_q8k_ws needs for R weight rows, C columns, M activation rows
+ * (0 for invalid sizes). */
+size_t kq_gemm_q8k_workspace(int R, int C, int M);
 
 /*
  * kq_gemm_q8k with a caller-provided workspace (ws 256-byte aligned, ws_bytes at least
- * kq_gemm_q8k_workspace(C, M), about M*C bytes with M rounded up to 256).  The call first copies
- * the activation quants into ws in MFMA fragment order, so that every operand load of the GEMM is
- * one contiguous 1 KB.  Allocates nothing; calls sharing a workspace must be ordered (same stream
- * or synchronised).
+ * kq_gemm_q8k_workspace(R, C, M): about M*C bytes with M rounded up to 256, plus S*M*R*4 bytes when
+ * the output tiles (64 rows x 128 tokens) are too few to fill the GPU and the K dimension is split
+ * S ways (S <= 8, at least 4 super-blocks each; fixed by R, C and M)).  The call first copies the
+ * activation quants into ws in MFMA fragment order, so that every operand load of the GEMM is one
+ * contiguous 1 KB; a split GEMM writes S partial sums into ws and adds them in order.  The result
+ * depends only on the inputs and (R, C, M); it equals kq_gemm_q8k's bit for bit when S = 1 and
+ * within the 1e-5 bar otherwise (fp32 sums in another order).  Allocates nothing; calls sharing a
+ * workspace must be ordered (same stream or synchronised).
  */
 int kq_gemm_q8k_ws(const void* w, int R, int C, int type, const void* xq, int M, float* y,
                    int64_t ldy, void* ws, size_t ws_bytes, void* stream);

@@ -238,9 +238,9 @@ int kq_gemm_q8k(const void* w, int R, int C, int type, const void* xq, int M, fl
     return check_launch(fn);
 }
 
-size_t kq_gemm_q8k_workspace(int C, int M) {
-    if (C < 256 || M < 1) return 0;
-    return gemm_q8k_workspace(C, M);
+size_t kq_gemm_q8k_workspace(int R, int C, int M) {
+    if (R < 8 || R % 8 || C < 256 || C % 256 || M < 1) return 0;
+    return gemm_q8k_workspace(R, C, M);
 }
 
 int kq_gemm_q8k_ws(const void* w, int R, int C, int type, const void* xq, int M, float* y,
@@ -248,7 +248,7 @@ int kq_gemm_q8k_ws(const void* w, int R, int C, int type, const void* xq, int M,
     static const char* fn = "kq_gemm_q8k_ws";
     KQ_TRY(check_gemm(w, R, C, type, xq, M, y, ldy, fn));
     KQ_TRY(check_ptr(ws, 256, "ws", fn));
-    const size_t need = gemm_q8k_workspace(C, M);
+    const size_t need = gemm_q8k_workspace(R, C, M);
     if (ws_bytes < need) return fail(KQ_ERR_ARG, "%s: workspace of %zu bytes, %zu needed", fn, ws_bytes, need);
     launch_gemm_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), M, y, ldy,
                     static_cast<uint8_t*>(ws), as_stream(stream));

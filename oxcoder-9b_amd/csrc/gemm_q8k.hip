@@ -35,6 +35,12 @@
 // the fragments are read from the Q8_K rows directly.  The next super-block's raw weight bytes
 // and activation fragments are loaded one step ahead.  Rows past M or R are clamped for loading
 // and not stored.
+//
+// K split.  When the output tiles are too few to fill the GPU (small M, or few weight rows), each
+// tile is computed by S workgroups (grid z), each over a contiguous range of super-blocks, into
+// S partial planes of the workspace; k_gemm_reduce then adds the planes in order s = 0, 1, ...
+// The split depends only on (R, C, M), so results are deterministic; it needs the workspace, so
+// kq_gemm_q8k (no workspace) never splits.
 #include <type_traits>
 
 #include "kq_device.h"
@@ -273,7 +279,8 @@ __device__ __forceinline__ void stage_x(const RawX<XP>& r, int mr, int xp, GemmB
 template <int TYPE, int BN, int WN, int WM, bool FRAG>
 __global__ void __launch_bounds__(64 * WN * WM)
 k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restrict__ XQ,
-           const uint8_t* __restrict__ XF, int M, float* __restrict__ Y, int64_t ldy) {
+           const uint8_t* __restrict__ XF, int M, float* __restrict__ Y, int64_t ldy, int gps,
+           float* __restrict__ P, int64_t pstride) {
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     constexpr int BM = 64 * WM;
     constexpr int NTHR = 64 * WN * WM;
@@ -292,6 +299,11 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     const int half = lane >> 5, l32 = lane & 31;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
+    // super-blocks [gbeg, gend) of the K split (all of them when gridDim.z == 1); with P the sums go
+    // to partial plane blockIdx.z (rows of R floats) instead of Y
+    const int gbeg = blockIdx.z * gps, gend = gbeg + gps < G ? gbeg + gps : G;
+    float* const Yo = P ? P + (int64_t)blockIdx.z * pstride : Y;
+    const int64_t ldo = P ? (int64_t)R : ldy;
 
     // A operand of this lane for K step ks of super-block g: afrag[mt] + g * AG + ks * AK
     constexpr int AG = FRAG ? 8192 : Q8K_BYTES, AK = FRAG ? 1024 : 32;
@@ -324,16 +336,17 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     RawW<TYPE, PPR> raw;
     RawX<XP> rx;
     v4i afr[2][8];
-    load_raw(raw, wrow, pi);
-    load_x(rx, xstage, xp);
+    load_raw(raw, wrow + (int64_t)gbeg * 8 * BS, pi);
+    load_x(rx, xstage + (int64_t)gbeg * Q8K_BYTES, xp);
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + ks * AK));
+        for (int ks = 0; ks < 8; ks++)
+            afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gbeg * AG + ks * AK));
     unpack(raw, pi, prow, LB0);
     stage_x<TYPE>(rx, mr, xp, LB0);
     {
-        const int g1 = G > 1 ? 1 : 0;
+        const int g1 = gbeg + 1 < gend ? gbeg + 1 : gbeg;
         load_raw(raw, wrow + (int64_t)g1 * 8 * BS, pi);
         load_x(rx, xstage + (int64_t)g1 * Q8K_BYTES, xp);
     }
@@ -347,8 +360,8 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
         constexpr int cur = decltype(cur_c)::value;
         GemmBuf<BN, BM>& Lc = cur ? LB1 : LB0;   // read this step
         GemmBuf<BN, BM>& Ln = cur ? LB0 : LB1;   // filled for the next step
-        const int gn = g + 1 < G ? g + 1 : G - 1;
-        const int g2 = g + 2 < G ? g + 2 : G - 1;
+        const int gn = g + 1 < gend ? g + 1 : gend - 1;
+        const int g2 = g + 2 < gend ? g + 2 : gend - 1;
 
         // ---- stage super-block g+1 into the other buffer (last iteration: a harmless repeat),
         //      then fetch the raw bytes of g+2
@@ -415,9 +428,9 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
         epilogue(1);
         __syncthreads();
     };
-    for (int g = 0; g < G; g += 2) {
+    for (int g = gbeg; g < gend; g += 2) {
         step(std::integral_constant<int, 0>{}, g);
-        if (g + 1 < G) step(std::integral_constant<int, 1>{}, g + 1);
+        if (g + 1 < gend) step(std::integral_constant<int, 1>{}, g + 1);
     }
 
     // ---- store
@@ -427,7 +440,7 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
 #pragma unroll
         for (int a = 0; a < 16; a++) {
             const int m = m0 + 64 * wm + 32 * mt + (a >> 2) * 8 + half * 4 + (a & 3);
-            if (m < M && n < R) Y[(int64_t)m * ldy + n] = yacc[mt][a];
+            if (m < M && n < R) Yo[(int64_t)m * ldo + n] = yacc[mt][a];
         }
 }
 
@@ -449,38 +462,109 @@ k_q8k_frag(const uint8_t* __restrict__ XQ, int M, int G, uint8_t* __restrict__ X
     }
 }
 
-size_t gemm_q8k_workspace(int C, int M) {
-    return (size_t)((M + GM_BMAX - 1) / GM_BMAX) * GM_BMAX * (size_t)C;
+// Partial planes y_s[m][r] of the K split, added in order s = 0 .. S-1: y = ((y_0 + y_1) + y_2) + ...
+// One thread per 4 consecutive outputs of a row.
+__global__ void __launch_bounds__(256)
+k_gemm_reduce(const float* __restrict__ P, int S, int64_t pstride, int M, int R, float* __restrict__ Y,
+              int64_t ldy) {
+    const int r4 = R >> 2;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)M * r4) return;
+    const int m = (int)(i / r4), r = (int)(i - (int64_t)m * r4) * 4;
+    const float* p = P + (int64_t)m * R + r;
+    f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    for (int s = 1; s < S; s++) {
+        const f32x4 b = *reinterpret_cast<const f32x4*>(p + s * pstride);
+        a = f32x4{__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z), __fadd_rn(a.w, b.w)};
+    }
+    *reinterpret_cast<f32x4_a4*>(Y + (int64_t)m * ldy + r) = a;
+}
+
+// Tiles of the launch below: 64 weight rows x 128 tokens.
+constexpr int GM_TN = 64, GM_TM = 128;
+// Workgroups that fill the GPU: two per CU of the 256 on an MI355X (fixed, so the split and the
+// workspace size do not depend on the device).  Measured (us, unsplit -> split): 4096x12288 Q6_K
+// at M = 32 / 64 / 128 / 256 / 512: 91.7 / 93.4 / 98.4 / 99.9 / 103.2 -> 34.6 / 35.9 / 38.1 /
+// 57.8 / 96.1; 12288x4096 Q4_K at M = 32 / 64: 33.6 / 33.5 -> 31.5 / 33.0.
+constexpr int GM_FILL = 512;
+constexpr int GM_SPLIT_MIN = 4;     // super-blocks per split, at least
+#ifndef KQ_GEMM_SPLIT_MAX
+#define KQ_GEMM_SPLIT_MAX 8
+#endif
+constexpr int GM_SPLIT_MAX = KQ_GEMM_SPLIT_MAX;
+
+// Super-blocks per split (gps) and splits (S) for a GEMM of R rows, C columns, M tokens.
+static void gemm_split(int R, int C, int M, int& S, int& gps) {
+    const int G = C / QK;
+    const int64_t tiles = (int64_t)((R + GM_TN - 1) / GM_TN) * ((M + GM_TM - 1) / GM_TM);
+    S = 1;
+    if (tiles < GM_FILL) {
+        int64_t want = GM_FILL / tiles;              // all S x tiles workgroups resident at once
+        // a 2- or 3-way split (the grid already covers more than half the CUs) of a short K saves
+        // less than adding the partial sums costs (12288x4096, M = 128: 36.6 against 34.6 us)
+        if (want < 4 && G < 32) want = 1;
+        want = want < GM_SPLIT_MAX ? want : GM_SPLIT_MAX;
+        const int most = G / GM_SPLIT_MIN;
+        S = (int)(want < most ? want : most);
+        if (S < 1) S = 1;
+    }
+    gps = (G + S - 1) / S;
+    S = (G + gps - 1) / gps;        // no empty split
+}
+
+static size_t frag_bytes(int C, int M) { return (size_t)((M + GM_BMAX - 1) / GM_BMAX) * GM_BMAX * (size_t)C; }
+
+size_t gemm_q8k_workspace(int R, int C, int M) {
+    int S, gps;
+    gemm_split(R, C, M, S, gps);
+    const size_t f = (frag_bytes(C, M) + 255) / 256 * 256;
+    return S > 1 ? f + (size_t)S * M * R * sizeof(float) : f;
 }
 
 template <int TYPE, int BN, int WN, int WM>
 static void launch_tile(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
-                        int64_t ldy, hipStream_t s) {
+                        int64_t ldy, int S, int gps, float* part, hipStream_t s) {
     constexpr int BM = 64 * WM;
-    dim3 grid((R + BN - 1) / BN, (M + BM - 1) / BM), block(64 * WN * WM);
-    if (xf) hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
-    else hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy);
+    static_assert(BN == GM_TN && BM == GM_TM, "the split rule assumes these tiles");
+    dim3 grid((R + BN - 1) / BN, (M + BM - 1) / BM, S), block(64 * WN * WM);
+    const int64_t pstride = (int64_t)M * R;
+    if (xf)
+        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy, gps,
+                           part, pstride);
+    else
+        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy, gps,
+                           part, pstride);
+    if (part) {
+        const int64_t n4 = (int64_t)M * (R / 4);
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, part, S, pstride, M,
+                           R, y, ldy);
+    }
 }
 
 template <int TYPE>
 static void launch_type(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
-                        int64_t ldy, hipStream_t s) {
+                        int64_t ldy, int S, int gps, float* part, hipStream_t s) {
     // 128 tokens x 64 weight rows per workgroup of 4 waves (80 KB of LDS, at most 256 VGPRs), so two
     // workgroups share a CU and each SIMD holds two waves: one wave's unpack and epilogue run under
     // the other's MFMAs.  (Measured against 128 x 128 tiles, one wave per SIMD, 4-8 waves per
     // workgroup: 289-317 against 331-379 us at M = 2048.)
-    launch_tile<TYPE, 64, 2, 2>(w, R, G, xq, xf, M, y, ldy, s);
+    launch_tile<TYPE, 64, 2, 2>(w, R, G, xq, xf, M, y, ldy, S, gps, part, s);
 }
 
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
                      uint8_t* ws, hipStream_t s) {
     const int G = C / QK;
+    int S = 1, gps = G;
+    float* part = nullptr;
     if (ws) {
         dim3 fgrid((M + GM_BMAX - 1) / GM_BMAX * (GM_BMAX / 32), G);
         hipLaunchKernelGGL(k_q8k_frag, fgrid, dim3(256), 0, s, xq, M, G, ws);
+        gemm_split(R, C, M, S, gps);
+        if (S > 1) part = reinterpret_cast<float*>(ws + (frag_bytes(C, M) + 255) / 256 * 256);
+        else gps = G;
     }
-    if (type == TYPE_Q4_K) launch_type<TYPE_Q4_K>(w, R, G, xq, ws, M, y, ldy, s);
-    else launch_type<TYPE_Q6_K>(w, R, G, xq, ws, M, y, ldy, s);
+    if (type == TYPE_Q4_K) launch_type<TYPE_Q4_K>(w, R, G, xq, ws, M, y, ldy, S, gps, part, s);
+    else launch_type<TYPE_Q6_K>(w, R, G, xq, ws, M, y, ldy, S, gps, part, s);
 }
 
 }  // namespace kq

@@ -39,9 +39,9 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
 // Small-batch GEMV on MFMA (C <= 16384, N <= 16): rows bit-identical to the GEMV above.
 void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
                             int N, float* const* y, const int64_t* ldy, hipStream_t s);
-// Prefill GEMM; ws (or nullptr) holds gemm_q8k_workspace(C, M) bytes (16-byte aligned) for the
-// activation fragments.
-size_t gemm_q8k_workspace(int C, int M);
+// Prefill GEMM; ws (or nullptr) holds gemm_q8k_workspace(R, C, M) bytes (256-byte aligned): the
+// activation fragments and, for grids too small to fill the GPU, the partial sums of the K split.
+size_t gemm_q8k_workspace(int R, int C, int M);
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
                      uint8_t* ws, hipStream_t s);
 // Argmax (argmax_block.h): ws holds argmax_workspace_bytes() bytes, its first word zero.

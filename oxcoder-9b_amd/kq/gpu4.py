@@ -185,7 +185,7 @@ class Engine:
         """Prefill GEMM over M rows of X [M][C] (M <= max_rows of the engine workspace)."""
         M, C = X.shape
         xq = self._quantize(X, C)
-        need = ops.gemm_workspace_bytes(C, M) + 256
+        need = max(ops.gemm_workspace_bytes(self.w[name][1], C, M) for name in names) + 256
         if self.gemm_ws is None or self.gemm_ws.numel() < need:
             self.gemm_ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         for name, y in zip(names, outs):

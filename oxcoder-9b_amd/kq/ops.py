@@ -185,14 +185,15 @@ def gemv_q8k_multi(mats, xq, N, ys):
     return ys
 
 
-def gemm_workspace_bytes(C_, M):
-    """Device bytes of the activation-fragment workspace a prefill GEMM of M rows x C_ needs."""
-    return int(_lib.kq().kq_gemm_q8k_workspace(C_, M))
+def gemm_workspace_bytes(R, C_, M):
+    """Device bytes of workspace a prefill GEMM of R weight rows x C_ columns over M activation rows
+    needs (activation fragments, and the K split's partial sums when it splits)."""
+    return int(_lib.kq().kq_gemm_q8k_workspace(R, C_, M))
 
 
-def gemm_workspace(C_, M, device):
+def gemm_workspace(R, C_, M, device):
     """A workspace tensor for gemm_q8k (kq_gemm_q8k_workspace bytes, 256-byte aligned)."""
-    return torch.empty(gemm_workspace_bytes(C_, M) + 256, dtype=torch.uint8, device=device)
+    return torch.empty(gemm_workspace_bytes(R, C_, M) + 256, dtype=torch.uint8, device=device)
 
 
 def _aligned(ws, n):
@@ -215,7 +216,7 @@ def gemm_q8k(w, R, C_, ty, xq, M, y, ldy=None, ws=None):
         _lib.check(_lib.kq().kq_gemm_q8k(pw, R, C_, ty, px, M, py, ldy, st))
     else:
         _dev(ws, "ws", torch.uint8)
-        pws, nws = _aligned(ws, gemm_workspace_bytes(C_, M))
+        pws, nws = _aligned(ws, gemm_workspace_bytes(R, C_, M))
         _lib.check(_lib.kq().kq_gemm_q8k_ws(pw, R, C_, ty, px, M, py, ldy, pws, nws, st))
     return y
 

@@ -230,12 +230,49 @@ def test_gemm_q8k_vs_oracle(dev, orc, ty, R, C, M):
     got = host(y)
     assert np.all(got[:, R:] == -3.0)
     assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C, ty, xq, M))
-    # the fragment-order path (caller workspace) gives the same bits
+    # the fragment-order path (caller workspace) gives the same bits unless it splits K
     y2 = torch.full((M, R + 8), -4.0, device=dev)
-    ops.gemm_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), M, y2, R + 8, ws=ops.gemm_workspace(C, M, dev))
+    ops.gemm_q8k(dev_t(W, dev), R, C, ty, dev_t(xq, dev), M, y2, R + 8, ws=ops.gemm_workspace(R, C, M, dev))
     got2 = host(y2)
-    np.testing.assert_array_equal(got2[:, :R], got[:, :R])
+    if gemm_splits_k(R, C, M):
+        assert_close_inf(got2[:, :R], orc.gemv_q8k(W, R, C, ty, xq, M))
+    else:
+        np.testing.assert_array_equal(got2[:, :R], got[:, :R])
     assert np.all(got2[:, R:] == -4.0)
+
+
+def gemm_splits_k(R, C, M):
+    """Whether kq_gemm_q8k_ws splits K for this shape: its workspace then holds partial sums beyond
+    the activation fragments (M rounded up to 256 rows of C bytes)."""
+    return ops.gemm_workspace_bytes(R, C, M) > -(-M // 256) * 256 * C
+
+
+@pytest.mark.parametrize("ty,R,C,M,S", [
+    (14, 1024, 12288, 64, 8),     # 16 tiles: 8 splits of 6 super-blocks
+    (12, 1024, 4096, 100, 4),     # 4 splits of 4
+    (12, 2048, 4352, 130, 4),     # G = 17: splits of 5, 5, 5, 2
+    (14, 512, 2048, 257, 2),      # G = 8: 2 splits of 4, three token tiles
+])
+def test_gemm_q8k_split_k(dev, orc, ty, R, C, M, S):
+    """Grids too small to fill the GPU split K over S workgroups per tile and add the partial sums
+    in a fixed order: within the bar of the oracle, the same bits call after call, columns past R
+    untouched."""
+    need = ops.gemm_workspace_bytes(R, C, M)
+    frag = -(-M // 256) * 256 * C
+    assert need == -(-frag // 256) * 256 + S * M * R * 4
+    W = synth(R, C, ty, 77)
+    xq = orc.quantize_q8k(kqq.synthetic_activations(M, C, seed=M + 5))
+    wd, xqd = dev_t(W, dev), dev_t(xq, dev)
+    ws = ops.gemm_workspace(R, C, M, dev)
+    y = torch.full((M, R + 16), -5.0, device=dev)
+    ops.gemm_q8k(wd, R, C, ty, xqd, M, y, R + 16, ws=ws)
+    got = host(y)
+    assert np.all(got[:, R:] == -5.0)
+    assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C, ty, xq, M))
+    ws.fill_(0x7f)                                  # stale partials from elsewhere must not matter
+    y2 = torch.full((M, R + 16), -6.0, device=dev)
+    ops.gemm_q8k(wd, R, C, ty, xqd, M, y2, R + 16, ws=ws)
+    np.testing.assert_array_equal(host(y2)[:, :R], got[:, :R])
 
 
 @pytest.mark.parametrize("ty", [12, 14])
@@ -256,7 +293,8 @@ def test_gemm_q8k_ws_matches_direct(dev, orc, ty):
     R, C = 264, 1024
     W = synth(R, C, ty, 41)
     wd = dev_t(W, dev)
-    ws = ops.gemm_workspace(C, 300, dev)
+    ws = ops.gemm_workspace(R, C, 300, dev)
+    assert not gemm_splits_k(R, C, 300) and not gemm_splits_k(R, C, 77)
     for M in (300, 77):
         xq = orc.quantize_q8k(kqq.synthetic_activations(M, C, seed=900 + M))
         xqd = dev_t(xq, dev)
@@ -273,7 +311,7 @@ def test_gemm_q8k_ws_rejects_small_or_misaligned_workspace(dev):
     w = dev_t(synth(R, C, 12, 5), dev)
     xq = torch.zeros(M * (C // 256) * 292, dtype=torch.uint8, device=dev)
     y = torch.empty((M, R), device=dev)
-    need = ops.gemm_workspace_bytes(C, M)
+    need = ops.gemm_workspace_bytes(R, C, M)
     assert need == 256 * C          # M rounded up to 128 rows, one byte per quant
     small = torch.empty(need, dtype=torch.uint8, device=dev)
     lib = _lib.kq()

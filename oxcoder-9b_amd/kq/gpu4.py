@@ -64,7 +64,7 @@ class Engine:
         self.max_rows = max_rows
         # Q8_K workspace, preallocated like the reference's device scratch (gpu4.py:70-79).
         self.xq = torch.empty(max_rows * (cols // QK) * Q8K_BYTES, dtype=torch.uint8, device=self.device)
-        self.gemm_ws = None   # activation-fragment workspace of the prefill GEMM, grown on demand
+        self.gemm_ws = None   # prefill GEMM workspace (activation fragments, K-split partial sums), grown on demand
 
     def _check_out(self, y, R, N=1):
         need = (N - 1) * (y.stride(0) if y.dim() == 2 else R) + R

@@ -162,3 +162,27 @@ def test_engine_feed_rows_dispatch(layer, dev):
     assert torch.equal(y40, ref)
     fp = eng.fingerprint()
     assert len(fp["libkq"]) == 16 and fp["mode"] == "q8k"
+
+
+def test_engine_prefill_gemm_split_k_layer(layer, dev):
+    """A 48-token prefill chunk through Engine.gemm for matrices of different R sharing one
+    workspace: q/k/v (grids of 64 and 16 tiles: K split 4 ways) and down (K split 8 ways).  Every
+    row is within the bar of its one-token GEMV, and a second call gives the same bits."""
+    w, _ = layer
+    eng = Engine(w, mode="q8k", max_rows=64)
+    M = 48
+    for names, C in ((["attn_q", "attn_k", "attn_v"], 4096), (["ffn_down"], 12288)):
+        X = torch.from_numpy(kqq.synthetic_activations(M, C, seed=C + 3)).to(dev)
+        outs = [torch.empty((M, w[n][1]), device=dev) for n in names]
+        assert eng.gemm(names, X, outs) == 1
+        again = [torch.empty_like(o) for o in outs]
+        eng.gemm(names, X, again)
+        for n, y, y2 in zip(names, outs, again):
+            R = w[n][1]
+            ref = torch.empty((16, R), device=dev)
+            for r0 in range(0, M, 16):
+                eng.gemv_batch([n], X[r0:r0 + 16], [ref])
+                want = ref.cpu().numpy()
+                got = y[r0:r0 + 16].cpu().numpy()
+                assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max(), (n, r0)
+            assert torch.equal(y, y2), n

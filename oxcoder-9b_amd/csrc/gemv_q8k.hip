@@ -357,7 +357,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
 // AMAX (one matrix, one token, one pass): the argmax of the outputs as well, into *aout
 // (argmax_block.h; aws is its workspace).
 template <int TYPE, int NT, int RPW, bool AMAX>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
 k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units, int P, int kmax,
                  uint8_t* aws, int* aout) {
     constexpr int WPT = 8 / RPW;

@@ -147,3 +147,37 @@ def test_source_hash_is_the_built_sources():
     spec.loader.exec_module(b)
     h = _lib.kq().kq_source_hash().decode()
     assert len(h) == 16 and h == b.source_hash()
+
+
+def _split_rule(R, C, M):
+    """The K-split rule kq_gemm_q8k_ws documents: tiles of 64 rows x 128 tokens; S = floor(512 /
+    tiles), at most 8 and at most G/4; a 2- or 3-way split only when G >= 32."""
+    G = C // 256
+    tiles = -(-R // 64) * -(-M // 128)
+    S = 1
+    if tiles < 512:
+        want = 512 // tiles
+        if want < 4 and G < 32:
+            want = 1
+        S = max(1, min(want, 8, G // 4))
+    gps = -(-G // S)
+    return -(-G // gps)
+
+
+def test_gemm_workspace_follows_the_split_rule():
+    """kq_gemm_q8k_workspace (host only, no GPU): fragment bytes (M rounded up to 256 rows of C
+    bytes, 256-byte aligned) plus S * M * R * 4 when K is split; 0 for invalid sizes."""
+    from kq import _lib
+    lib = _lib.kq()
+    rng = np.random.default_rng(3)
+    shapes = [(12288, 4096, 512), (4096, 12288, 512), (4096, 12288, 64), (4096, 4096, 64), (1024, 4096, 1),
+              (12288, 4096, 2048), (8, 256, 1), (136, 256, 300), (2048, 4352, 130), (151936, 4096, 16)]
+    shapes += [(8 * int(rng.integers(1, 3000)), 256 * int(rng.integers(1, 60)), int(rng.integers(1, 4000)))
+               for _ in range(300)]
+    for R, C, M in shapes:
+        S = _split_rule(R, C, M)
+        frag = -(-M // 256) * 256 * C
+        want = -(-frag // 256) * 256 + (S * M * R * 4 if S > 1 else 0)
+        assert lib.kq_gemm_q8k_workspace(R, C, M) == want, (R, C, M, S)
+    for R, C, M in [(0, 4096, 8), (12, 4096, 8), (64, 0, 8), (64, 300, 8), (64, 4096, 0)]:
+        assert lib.kq_gemm_q8k_workspace(R, C, M) == 0, (R, C, M)

@@ -181,3 +181,13 @@ def test_gemm_workspace_follows_the_split_rule():
         assert lib.kq_gemm_q8k_workspace(R, C, M) == want, (R, C, M, S)
     for R, C, M in [(0, 4096, 8), (12, 4096, 8), (64, 0, 8), (64, 300, 8), (64, 4096, 0)]:
         assert lib.kq_gemm_q8k_workspace(R, C, M) == 0, (R, C, M)
+
+
+def test_missing_library_raises(monkeypatch):
+    """No fallback: without the built library every entry point raises."""
+    from kq import _lib, ops
+    monkeypatch.setattr(_lib, "LIBKQ", "/nonexistent/libkq.so")
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.kq()
+    with pytest.raises(RuntimeError, match="not built"):
+        ops.gemm_workspace_bytes(4096, 4096, 512)

@@ -108,7 +108,8 @@ def test_subblock_sums_reference_inputs(dev, orc, ty):
     np.testing.assert_array_equal(got, orc.subblock_sums(W, R, C, ty, xq, 3))
 
 
-@pytest.mark.parametrize("ty,R,C", [(12, 64, 4096), (14, 64, 4096), (12, 16, 4352), (14, 24, 12288)])
+@pytest.mark.parametrize("ty,R,C", [(12, 64, 4096), (14, 64, 4096), (12, 16, 4352), (14, 24, 12288),
+                                    (12, 16, 61440)])
 def test_subblock_sums_synthetic(dev, orc, ty, R, C):
     W = synth(R, C, ty, 5)
     xq = orc.quantize_q8k(kqq.synthetic_activations(2, C, seed=5))
@@ -137,6 +138,9 @@ GEMV_SHAPES = [
     (12, 1024, 4096), (12, 12288, 4096),   # k/v and gate/up shapes
     (14, 4096, 12288),                     # Q6_K down
     (14, 1024, 4096),                      # Q6_K attn_v
+    (12, 64, 12288),                       # Q4_K, three passes on the pass-split kernel
+    (14, 48, 8192), (14, 16, 8448),        # Q6_K: two passes (split kernel); three, the last one column
+    (12, 16, 61440), (14, 8, 61440),       # the largest C: 15 passes, sequential kernel, full pass tree
 ]
 
 
@@ -252,6 +256,7 @@ def gemm_splits_k(R, C, M):
     (12, 1024, 4096, 100, 4),     # 4 splits of 4
     (12, 2048, 4352, 130, 4),     # G = 17: splits of 5, 5, 5, 2
     (14, 512, 2048, 257, 2),      # G = 8: 2 splits of 4, three token tiles
+    (14, 64, 61440, 40, 8),       # the largest C: 8 splits of 30 super-blocks
 ])
 def test_gemm_q8k_split_k(dev, orc, ty, R, C, M, S):
     """Grids too small to fill the GPU split K over S workgroups per tile and add the partial sums
@@ -338,7 +343,8 @@ def test_gemv_f32_reference_unit_test(dev, orc, ty):
     assert_close_inf(got, orc.matvec_f32(W, R, C, ty, x).astype(np.float64))
 
 
-@pytest.mark.parametrize("ty,R,C", [(12, 4096, 4096), (14, 4096, 12288), (12, 40, 4352), (14, 8, 256)])
+@pytest.mark.parametrize("ty,R,C", [(12, 4096, 4096), (14, 4096, 12288), (12, 40, 4352), (14, 8, 256),
+                                    (12, 16, 61440), (14, 8, 61440)])
 def test_gemv_f32_vs_oracle(dev, orc, ty, R, C):
     W = synth(R, C, ty, 3 * R + ty)
     x = kqq.synthetic_activations(1, C, seed=C + 1)[0]

@@ -211,7 +211,7 @@ def traffic_from_profile(path=os.path.join(ROOT, "profiles", "gemv_q4k_decode_la
 
 def cpu_baseline(budget_s=12.0, budget_2t_s=6.0, runs=5):
     """The reference's CPU path (kc_matvec, fp32 activations) on the same layer shapes: `runs` timed
-    runs after one warm-up, median, at the box's CPU share (16 threads unless KQ_CPU_THREADS or
+    runs after one warm-up, median, at the host's CPU share for one GPU (16 threads unless KQ_CPU_THREADS or
     OMP_NUM_THREADS says otherwise) and at 2 threads (the reference's validated default,
     scripts/kindi_q4/kindi/cpu4.py:99)."""
     from kq import quantize as kqq
@@ -457,8 +457,8 @@ def main():
                          "kernel); 'gemm' runs each prefill GEMM shape twice")
     a = ap.parse_args()
     if a.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the products shard by "
-              "output rows with no exchange; see the design notes). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: the library has no multi-GPU path (the products would shard by "
+              "output rows, with one all-reduce per token for o and down). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -1,7 +1,7 @@
 /*
  * kq_oracle.c -- CPU oracle for the Kindi Q4 quantized matrix products.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker: tests/, the smoke check
+ * TEST INFRASTRUCTURE ONLY.  This file is the oracle: tests/, the smoke check
  * and the CPU-baseline leg of bench.py may call it.  Nothing in the product
  * library (libkq.so) links it, and no product code path falls back to it.
  *

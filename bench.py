@@ -334,6 +334,66 @@ def producers_extra(torch, rn, layers, dev, steps=320):
     return out
 
 
+def pack_extra(torch, dev, layers=2):
+    """Pack loading (the F3 path, gpu4.Weights over a Kindi pack): write a pack with the 9B profile's
+    dimensions for `layers` layers plus the 248320-row embedding and head (random block bytes: the
+    loader does not look inside blocks), check it with verify_pack (full: sizes, sha256, shapes),
+    then bring every quantized tensor to the device through PackWeights twice: with the file in the
+    host page cache, and after asking the kernel to drop its pages (POSIX_FADV_DONTNEED; no effect
+    where the temporary directory is memory-backed)."""
+    import shutil
+    import tempfile
+    from kq import pack
+    shapes = pack.profile_shapes(layers)
+    dims = dict(pack.PROFILE_DIMS, layers=layers)
+    rng = np.random.default_rng(7)
+    tensors = {}
+    for name, (R, C_) in shapes.items():
+        if pack._float_storage(name, R):
+            tensors[name] = (rng.standard_normal(R * C_).astype(np.float32), R, C_, 0)
+        else:
+            ty = 14 if name.endswith(("output.weight", "ffn_down.weight")) else 12
+            nbytes = R * (C_ // 256) * (210 if ty == 14 else 144)
+            tensors[name] = (rng.integers(0, 256, nbytes, dtype=np.uint8), R, C_, ty)
+    root = tempfile.mkdtemp(prefix="kq_pack_", dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        path = os.path.join(root, "pack")
+        t0 = time.perf_counter()
+        pack.write_pack(path, tensors, dims=dims)
+        t_write = time.perf_counter() - t0
+        del tensors
+        wbin = os.path.join(path, "weights.bin")
+        fd = os.open(wbin, os.O_RDONLY)
+        os.fsync(fd)
+        t0 = time.perf_counter()
+        pack.verify_pack(path, full=True, dims=dims, shapes=shapes)
+        t_verify = time.perf_counter() - t0
+        qnames = [n for n, (R, _) in shapes.items() if not pack._float_storage(n, R)]
+        out = {}
+        for label, drop in (("page_cache", False), ("after_fadv_dontneed", True)):
+            if drop:
+                os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+            w = pack.PackWeights(path, device=dev)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            total = 0
+            for n in qnames:
+                buf = w[n][0]
+                total += buf.numel()
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t0
+            out[label] = {"GB/s": round(total / el / 1e9, 2), "s": round(el, 3)}
+            w.close()
+            del w
+            torch.cuda.empty_cache()
+        os.close(fd)
+        out.update({"bytes": total, "tensors": len(qnames), "layers": layers,
+                    "write_s": round(t_write, 2), "verify_full_s": round(t_verify, 2)})
+        return out
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+
+
 def head_extra(torch, rn, dev):
     """Output head 151936x4096 Q6_K with the greedy pick: fused (kq_gemv_q8k_argmax) against the GEMV
     followed by kq_argmax; two resident copies (1 GB) alternate so the cache does not serve them."""
@@ -529,6 +589,8 @@ def main():
         result["head"] = head_extra(torch, rn, dev)
         log("bench: full decode stream")
         result["decode_stream"] = decode_stream_extra(torch, rn, dev)
+        log("bench: pack loading")
+        result["pack_load"] = pack_extra(torch, dev)
     if not a.no_cpu:
         log("bench: CPU baseline")
         result["cpu_baseline"] = cpu_baseline()

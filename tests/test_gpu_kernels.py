@@ -351,3 +351,36 @@ def test_gemv_f32_vs_oracle(dev, orc, ty, R, C):
     y = torch.empty(R, device=dev)
     ops.gemv(dev_t(W, dev), R, C, ty, dev_t(x, dev), y)
     assert_close_inf(host(y), orc.matvec_f32(W, R, C, ty, x).astype(np.float64))
+
+
+def test_random_shapes_sweep(dev, orc):
+    """Seeded sweep over ragged shapes (R = 8..520, C = 256..8192, N = 1..16, M = 1..300, both types):
+    GEMV rows within the bar of the oracle and bit-equal to their one-token results; the GEMM (both
+    entry points, split or not) within the bar."""
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        ty = (12, 14)[case % 2]
+        R = 8 * int(rng.integers(1, 66))
+        C = 256 * int(rng.integers(1, 33))
+        N = int(rng.integers(1, 17))
+        M = int(rng.integers(1, 301))
+        W = synth(R, C, ty, 1000 + case)
+        Wd = dev_t(W, dev)
+        X = kqq.synthetic_activations(max(N, M), C, seed=2000 + case)
+        xq = orc.quantize_q8k(X)
+        xqd = dev_t(xq, dev)
+        tag = (case, ty, R, C, N, M)
+        yb = torch.empty((N, R), device=dev)
+        ops.gemv_q8k(Wd, R, C, ty, xqd, N, yb)
+        ref = orc.gemv_q8k(W, R, C, ty, xq[:N], N)
+        assert_close_inf(host(yb), ref)
+        y1 = torch.empty(R, device=dev)
+        n = int(rng.integers(0, N))
+        ops.gemv_q8k(Wd, R, C, ty, xqd[n:n + 1], 1, y1)
+        assert np.array_equal(host(y1), host(yb)[n]), tag
+        refm = orc.gemv_q8k(W, R, C, ty, xq[:M], M)
+        ym = torch.empty((M, R), device=dev)
+        ops.gemm_q8k(Wd, R, C, ty, xqd, M, ym)
+        assert_close_inf(host(ym), refm)
+        ops.gemm_q8k(Wd, R, C, ty, xqd, M, ym, ws=ops.gemm_workspace(R, C, M, dev))
+        assert_close_inf(host(ym), refm)

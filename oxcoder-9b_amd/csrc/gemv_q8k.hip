@@ -470,13 +470,15 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
 // Rows per wave: Q4_K 2 keeps per-wave register use moderate and gives many units to balance;
 // with several tokens per launch the register budget is NT*RPW <= 8 outputs per lane.  Q6_K
 // takes one row per wave: twice the units, so each wave walks more (unit, pass) steps and its
-// prefetch covers more of the stream (4096x12288 at one token: 12.3 us against 14.2 us at 2).
-static int pick_rpw(int nt, int type) {
+// prefetch covers more of the stream (the one-pass output head 151936x4096: 96 us against 102 us
+// at 2), except two tokens on the sequential kernel (3 or more passes), where 2 rows per wave
+// share each pass's activations (4096x12288: 12.9 -> 12.3 us; one token: no difference).
+static int pick_rpw(int nt, int type, int G) {
 #ifdef KQ_GEMV_RPW
-    (void)nt; (void)type;
+    (void)nt; (void)type; (void)G;
     return KQ_GEMV_RPW;
 #else
-    if (type == TYPE_Q6_K) return 1;
+    if (type == TYPE_Q6_K) return nt == 2 && (G + 15) / 16 > KQ_GEMV_SPLIT_MAX_Q6 ? 2 : 1;
     return nt >= 3 ? 1 : 2;
 #endif
 }
@@ -577,8 +579,8 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
         }
         for (int i = n; i < 4; i++) mg.first_unit[i] = tiles;
         const uint8_t* xg = xq + (int64_t)n0 * G * Q8K_BYTES;
-        if (type == TYPE_Q4_K) launch1<TYPE_Q4_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q4_K), s);
-        else launch1<TYPE_Q6_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q6_K), s);
+        if (type == TYPE_Q4_K) launch1<TYPE_Q4_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q4_K, G), s);
+        else launch1<TYPE_Q6_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q6_K, G), s);
     }
 }
 

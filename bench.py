@@ -374,6 +374,7 @@ def pack_extra(torch, dev, layers=2):
             if drop:
                 os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
             w = pack.PackWeights(path, device=dev)
+            w._staging()                                # pinned staging allocated once, not timed
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             total = 0

@@ -37,6 +37,8 @@ PROFILE_DIMS = {"layers": 32, "width": 4096, "ffn": 12288, "heads": 16, "kv_head
                 "full_attention_interval": 4}
 PINNED = ("token_embd.weight", "output.weight")
 STAGE_BYTES = 8 << 20
+READERS = 4              # host threads reading one large tensor (each: two pinned buffers, a stream)
+PARALLEL_MIN = 64 << 20  # tensors from this size are read by all READERS
 
 
 def profile_shapes(layers=32):
@@ -170,9 +172,13 @@ class PackWeights:
         self.limit = int(limit) if limit is not None else 1 << 62
         self.pin_boundaries = pin_boundaries
         self._stage = None
+        self._pool = None
         self._f32 = {}
 
     def close(self):
+        if self._pool is not None:
+            self._pool.shutdown(wait=True)
+            self._pool = None
         if self.fd is not None:
             os.close(self.fd)
             self.fd = None
@@ -184,10 +190,33 @@ class PackWeights:
         return name in self.index and self.index[name]["type"] in BLOCK
 
     def _staging(self):
+        """Per reader: two pinned staging buffers, their events and a copy stream (reader 0 copies on
+        the caller's stream)."""
         if self._stage is None:
-            self._stage = [torch.empty(STAGE_BYTES, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
-            self._events = [torch.cuda.Event(), torch.cuda.Event()]
+            self._stage = [[torch.empty(STAGE_BYTES, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+                           for _ in range(READERS)]
+            self._events = [[torch.cuda.Event(), torch.cuda.Event()] for _ in range(READERS)]
+            self._streams = [None] + [torch.cuda.Stream(device=self.device) for _ in range(READERS - 1)]
         return self._stage, self._events
+
+    def _read_range(self, t, buf, base, lo, hi):
+        """Bytes [lo, hi) of the tensor at file offset ``base`` into buf, by reader t: 8 MiB preads into
+        the reader's two pinned buffers, each copy to the device overlapping the next read."""
+        stage, events = self._stage[t], self._events[t]
+        stream = self._streams[t] or torch.cuda.current_stream(self.device)
+        with torch.cuda.stream(stream):
+            for i, off in enumerate(range(lo, hi, STAGE_BYTES)):
+                n = min(STAGE_BYTES, hi - off)
+                s, ev = stage[i % 2], events[i % 2]
+                ev.synchronize()                               # its previous copy has finished
+                view = memoryview(s.numpy())[:n]
+                if os.preadv(self.fd, [view], base + off) != n:
+                    raise IOError("Truncated Q4 weight tensor")
+                buf[off:off + n].copy_(s[:n], non_blocking=True)
+                ev.record(stream)
+        for ev in events:
+            ev.synchronize()
+        return hi - lo
 
     def _evict_for(self, size):
         protected = set(PINNED) if self.pin_boundaries else set()
@@ -208,20 +237,21 @@ class PackWeights:
         size = rec["bytes"]
         self._evict_for(size)
         buf = torch.empty(size, dtype=torch.uint8, device=self.device)
-        stage, events = self._staging()
-        stream = torch.cuda.current_stream(self.device)
-        for i, off in enumerate(range(0, size, STAGE_BYTES)):
-            n = min(STAGE_BYTES, size - off)
-            s, ev = stage[i % 2], events[i % 2]
-            ev.synchronize()                                   # its previous copy has finished
-            view = memoryview(s.numpy())[:n]
-            if os.preadv(self.fd, [view], rec["offset"] + off) != n:
-                raise IOError("Truncated Q4 weight tensor")
-            buf[off:off + n].copy_(s[:n], non_blocking=True)
-            ev.record(stream)
-            self.read_bytes += n
-        for ev in events:
-            ev.synchronize()
+        self._staging()
+        if size < PARALLEL_MIN or READERS < 2:
+            self.read_bytes += self._read_range(0, buf, rec["offset"], 0, size)
+        else:
+            # READERS contiguous ranges (whole staging chunks), read at once: the copies from the
+            # page cache (or the device's queue depth) bound a single reader
+            if self._pool is None:
+                import concurrent.futures as cf
+                self._pool = cf.ThreadPoolExecutor(READERS - 1)
+            chunks = (size + STAGE_BYTES - 1) // STAGE_BYTES
+            cut = [min(size, (chunks * t // READERS) * STAGE_BYTES) for t in range(READERS + 1)]
+            futs = [self._pool.submit(self._read_range, t, buf, rec["offset"], cut[t], cut[t + 1])
+                    for t in range(1, READERS)]
+            done = self._read_range(0, buf, rec["offset"], cut[0], cut[1])
+            self.read_bytes += done + sum(f.result() for f in futs)
         os.posix_fadvise(self.fd, rec["offset"], rec["padded_bytes"], os.POSIX_FADV_DONTNEED)
         value = (buf, int(rec["rows"]), int(rec["ne0"]), int(rec["type"]))
         self.cache[name] = value

@@ -72,3 +72,28 @@ def test_engine_on_pack_matches_in_memory_weights(dev, built, orc):
     np.testing.assert_array_equal(outs[0][1].cpu().numpy(),
                                   orc.dequant_row(tensors["token_embd.weight"][0], 2048, 4096, 12, 1234))
     pw.close()
+
+
+def test_large_tensor_read_by_several_readers(dev, tmp_path):
+    """A tensor from PARALLEL_MIN up is read by READERS host threads in contiguous ranges (the last
+    one partial): the device bytes equal the file's, and a second PackWeights on the same pack, read
+    while the first's cache holds the tensor, agrees."""
+    R, C = 21848, 4096                        # 21848 x 16 x 144 B = 50.3 MB: below the threshold
+    R2 = 47000                                 # Q6_K 47000 x 16 x 210 = 157.9 MB (not a multiple of 8 MiB)
+    rng = np.random.default_rng(5)
+    big = rng.integers(0, 256, R2 * 16 * 210, dtype=np.uint8)
+    small = rng.integers(0, 256, R * 16 * 144, dtype=np.uint8)
+    tensors = {"output.weight": (big, R2, C, 14), "token_embd.weight": (small, R, C, 12)}
+    p = tmp_path / "pack"
+    pack.write_pack(p, tensors, dims={"layers": 0, "width": 4096})
+    assert big.nbytes >= pack.PARALLEL_MIN and small.nbytes < pack.PARALLEL_MIN
+    w = pack.PackWeights(p, device=dev)
+    for name, (data, rows, ne0, ty) in tensors.items():
+        buf, r, c, t = w[name]
+        assert (r, c, t) == (rows, ne0, ty)
+        assert np.array_equal(buf.cpu().numpy(), data), name
+    assert w.read_bytes == big.nbytes + small.nbytes
+    w2 = pack.PackWeights(p, device=dev)
+    assert torch.equal(w2["output.weight"][0], w["output.weight"][0])
+    w.close()
+    w2.close()

@@ -12,7 +12,8 @@ A pack (scripts/kindi_q4/kindi/q4pack.py) is a directory with
 ``verify_pack`` applies the reference's checks (q4pack.py:86-108) in the same order with the same
 messages.  ``PackWeights`` is the device side of gpu4.Weights (gpu4.py:17-48): ``w[name] ->
 (buf, R, C, type)`` with ``buf`` a device uint8 tensor in the Kindi layout, read with 8 MiB
-preads through two pinned staging buffers whose copies overlap the next read, a least-recently
+preads through two pinned staging buffers whose copies overlap the next read (large tensors by
+several reader threads over contiguous ranges), a least-recently
 used byte budget that spares the embedding and the head, and POSIX_FADV_DONTNEED after each
 tensor so the host page cache does not keep a second copy.  On a 288 GB MI355X the default budget
 keeps the whole 9B pack (5.6 GB) resident.  ``write_pack`` builds a pack from tensors already in

@@ -10,7 +10,8 @@ A pack (scripts/kindi_q4/kindi/q4pack.py) is a directory with
                       files {name: {size, sha256}} (q4pack.py:163-174).
 
 ``verify_pack`` applies the reference's checks (q4pack.py:86-108) in the same order with the same
-messages.  ``PackWeights`` is the device side of gpu4.Weights (gpu4.py:17-48): ``w[name] ->
+messages; ``open_pack`` takes its full-or-size mode from KINDI_Q4_VERIFY unless told (q4pack.py:80-84,
+gpu4.py:55).``PackWeights`` is the device side of gpu4.Weights (gpu4.py:17-48): ``w[name] ->
 (buf, R, C, type)`` with ``buf`` a device uint8 tensor in the Kindi layout, read with 8 MiB
 preads through two pinned staging buffers whose copies overlap the next read (large tensors by
 several reader threads over contiguous ranges), a least-recently
@@ -85,6 +86,16 @@ def digest(path):
         for b in iter(lambda: f.read(4 << 20), b""):
             h.update(b)
     return h.hexdigest()
+
+
+def verification_full():
+    """The verification mode from KINDI_Q4_VERIFY (q4pack.py:80-84): "full" (the default when it is
+    unset) checks sizes and sha256, "size" checks sizes only; any other value is an error rather
+    than a silent choice."""
+    mode = os.environ.get("KINDI_Q4_VERIFY", "full")
+    if mode not in ("full", "size"):
+        raise ValueError("KINDI_Q4_VERIFY must be full or size")
+    return mode == "full"
 
 
 def verify_pack(pack, full=True, dims=PROFILE_DIMS, shapes=None):
@@ -273,7 +284,8 @@ class PackWeights:
         return self._f32[name]
 
 
-def open_pack(pack, full=True, limit=None, device="cuda", dims=PROFILE_DIMS, shapes=None):
-    """verify_pack, then a PackWeights over the pack (the Engine's weights, gpu4.py:59)."""
-    verify_pack(pack, full=full, dims=dims, shapes=shapes)
+def open_pack(pack, full=None, limit=None, device="cuda", dims=PROFILE_DIMS, shapes=None):
+    """verify_pack, then a PackWeights over the pack (the Engine's weights, gpu4.py:55-59).
+    ``full=None`` takes the mode from KINDI_Q4_VERIFY, as the Engine does."""
+    verify_pack(pack, full=verification_full() if full is None else full, dims=dims, shapes=shapes)
     return PackWeights(pack, limit=limit, device=device)

@@ -120,3 +120,57 @@ def test_profile_table_of_the_9b_model():
     assert len(floats) == 1 + 8 * 4 + 24 * 8
     quant = {n: rc for n, rc in s.items() if not pack._float_storage(n, rc[0])}
     assert all(r % 8 == 0 and c % 256 == 0 for r, c in quant.values())
+
+
+def test_rejects_manifest_traversal(tiny_pack):
+    """A manifest file name with a directory part is refused before any file is opened
+    (q4pack.py:92; tests/kindi_q4/test_pack_validation.py's traversal case)."""
+    man = json.loads((tiny_pack / "kindi_pack.json").read_text())
+    man["files"] = {"../x": {}}
+    (tiny_pack / "kindi_pack.json").write_text(json.dumps(man))
+    with pytest.raises(ValueError, match="Invalid manifest path"):
+        pack.verify_pack(tiny_pack, full=True, dims=TINY_DIMS, shapes=tiny_shapes())
+
+
+def test_rejects_the_9b_dimensions_changed(tiny_pack):
+    """A pack whose manifest dimensions differ from the 9B profile in one field is refused by the
+    default profile check before any tensor is read."""
+    man = json.loads((tiny_pack / "kindi_pack.json").read_text())
+    man["dimensions"] = dict(pack.PROFILE_DIMS, width=5120)
+    (tiny_pack / "kindi_pack.json").write_text(json.dumps(man))
+    with pytest.raises(ValueError, match="Unsupported Q4 profile"):
+        pack.verify_pack(tiny_pack)
+
+
+@pytest.mark.parametrize("mode,expected", [(None, True), ("full", True), ("size", False)])
+def test_verification_mode_is_explicit(monkeypatch, mode, expected):
+    if mode is None:
+        monkeypatch.delenv("KINDI_Q4_VERIFY", raising=False)
+    else:
+        monkeypatch.setenv("KINDI_Q4_VERIFY", mode)
+    assert pack.verification_full() is expected
+
+
+def test_verification_mode_typo_is_an_error(monkeypatch, tiny_pack):
+    monkeypatch.setenv("KINDI_Q4_VERIFY", "typo")
+    with pytest.raises(ValueError, match="KINDI_Q4_VERIFY must be full or size"):
+        pack.verification_full()
+    with pytest.raises(ValueError, match="KINDI_Q4_VERIFY must be full or size"):
+        pack.open_pack(tiny_pack, device="cpu", dims=TINY_DIMS, shapes=tiny_shapes())
+
+
+def test_open_pack_takes_the_mode_from_the_environment(monkeypatch, tiny_pack):
+    """A flipped byte keeps every size: "size" mode opens the pack, "full" mode finds the checksum
+    mismatch.  Opening reads no tensor, so this runs without a device."""
+    with open(tiny_pack / "weights.bin", "r+b") as f:
+        f.seek(100)
+        b = f.read(1)
+        f.seek(100)
+        f.write(bytes([b[0] ^ 1]))
+    monkeypatch.setenv("KINDI_Q4_VERIFY", "size")
+    w = pack.open_pack(tiny_pack, device="cpu", dims=TINY_DIMS, shapes=tiny_shapes())
+    assert "output.weight" in w
+    w.close()
+    monkeypatch.setenv("KINDI_Q4_VERIFY", "full")
+    with pytest.raises(ValueError, match="Pack checksum mismatch: weights.bin"):
+        pack.open_pack(tiny_pack, device="cpu", dims=TINY_DIMS, shapes=tiny_shapes())

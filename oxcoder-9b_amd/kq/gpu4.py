@@ -28,7 +28,7 @@ logits as it stores them (kq_gemv_q8k_argmax).
 import torch
 
 from . import ops
-from .formats import Q8K_BYTES, QK, check_shape
+from .formats import BLOCK, Q8K_BYTES, QK, check_shape
 
 
 class Weights:
@@ -52,6 +52,16 @@ class Weights:
         return name in self.cache
 
 
+def _widest(weights):
+    """Most columns of any quantized tensor the weights hold: from the pack index when there is
+    one (a PackWeights reads tensors lazily, so its cache starts empty), else from the resident
+    tensors."""
+    index = getattr(weights, "index", None)
+    if index is not None:
+        return max([r["ne0"] for r in index.values() if r["type"] in BLOCK] or [QK])
+    return max([C for (_, _, C, _) in weights.cache.values()] or [QK])
+
+
 class Engine:
     def __init__(self, weights, mode="q8k", max_cols=None, max_rows=16):
         if mode not in ("q8k", "f32"):
@@ -59,7 +69,7 @@ class Engine:
         self.w = weights
         self.mode = mode
         self.device = weights.device
-        cols = max_cols or max([C for (_, _, C, _) in weights.cache.values()] or [QK])
+        cols = max_cols or _widest(weights)
         self.max_cols = cols
         self.max_rows = max_rows
         # Q8_K workspace, preallocated like the reference's device scratch (gpu4.py:70-79).

@@ -60,7 +60,7 @@ def test_engine_on_pack_matches_in_memory_weights(dev, built, orc):
     x = torch.from_numpy(kqq.synthetic_activations(1, 4096, seed=4)[0]).to(dev)
     outs = []
     for w in (pw, mem):
-        eng = Engine(w, mode="q8k", max_cols=12288)
+        eng = Engine(w, mode="q8k")               # workspace sized from the pack index
         ys = [torch.empty(12288, device=dev), torch.empty(12288, device=dev)]
         eng.gemv(["blk.0.ffn_gate.weight", "blk.0.ffn_up.weight"], x, ys)
         emb = eng.embed(1234)

@@ -174,3 +174,18 @@ def test_open_pack_takes_the_mode_from_the_environment(monkeypatch, tiny_pack):
     monkeypatch.setenv("KINDI_Q4_VERIFY", "full")
     with pytest.raises(ValueError, match="Pack checksum mismatch: weights.bin"):
         pack.open_pack(tiny_pack, device="cpu", dims=TINY_DIMS, shapes=tiny_shapes())
+
+
+def test_engine_over_a_pack_sizes_its_workspace_from_the_index(tiny_pack):
+    """A PackWeights reads tensors lazily (its cache starts empty), so the Engine takes the widest
+    quantized tensor from the pack index: 512 columns (ffn_down) in the tiny pack.  No device
+    work: the engine's workspace is a host tensor here."""
+    from kq.gpu4 import Engine
+    w = pack.PackWeights(tiny_pack, device="cpu")
+    try:
+        assert len(w.cache) == 0
+        eng = Engine(w, mode="q8k")
+        assert eng.max_cols == 512
+        assert eng.xq.numel() == 16 * (512 // 256) * 292
+    finally:
+        w.close()

@@ -182,18 +182,22 @@ class Engine:
         N, C = X.shape
         if not 1 <= N <= 16:
             raise ValueError("batch of %d rows: 1..16 supported" % N)
+        if len(outs) < len(names):
+            raise ValueError("one output per matrix")
         xq = self._quantize(X, C)
         for name, y in zip(names, outs):
             w, R, C_, ty = self.w[name]
             if C_ != C:
                 raise ValueError("column count mismatch for " + name)
             self._check_out(y, R, N)
-            ops.gemv_q8k(w, R, C_, ty, xq, N, y, y.stride(0))
+            ops.gemv_q8k(w, R, C_, ty, xq, N, y, y.stride(0) if y.dim() == 2 else R)
         return 1
 
     def gemm(self, names, X, outs):
         """Prefill GEMM over M rows of X [M][C] (M <= max_rows of the engine workspace)."""
         M, C = X.shape
+        if len(outs) < len(names):
+            raise ValueError("one output per matrix")
         xq = self._quantize(X, C)
         need = max(ops.gemm_workspace_bytes(self.w[name][1], C, M) for name in names) + 256
         if self.gemm_ws is None or self.gemm_ws.numel() < need:
@@ -203,7 +207,7 @@ class Engine:
             if C_ != C:
                 raise ValueError("column count mismatch for " + name)
             self._check_out(y, R, M)
-            ops.gemm_q8k(w, R, C_, ty, xq, M, y, y.stride(0), ws=self.gemm_ws)
+            ops.gemm_q8k(w, R, C_, ty, xq, M, y, y.stride(0) if y.dim() == 2 else R, ws=self.gemm_ws)
         return 1
 
     def embed(self, tok, out=None, name="token_embd.weight"):

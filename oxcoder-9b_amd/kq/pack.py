@@ -10,16 +10,17 @@ A pack (scripts/kindi_q4/kindi/q4pack.py) is a directory with
                       files {name: {size, sha256}} (q4pack.py:163-174).
 
 ``verify_pack`` applies the reference's checks (q4pack.py:86-108) in the same order with the same
-messages; ``open_pack`` takes its full-or-size mode from KINDI_Q4_VERIFY unless told (q4pack.py:80-84,
-gpu4.py:55).``PackWeights`` is the device side of gpu4.Weights (gpu4.py:17-48): ``w[name] ->
-(buf, R, C, type)`` with ``buf`` a device uint8 tensor in the Kindi layout, read with 8 MiB
-preads through two pinned staging buffers whose copies overlap the next read (large tensors by
-several reader threads over contiguous ranges), a least-recently
-used byte budget that spares the embedding and the head, and POSIX_FADV_DONTNEED after each
-tensor so the host page cache does not keep a second copy.  On a 288 GB MI355X the default budget
+messages; ``open_pack`` takes its full-or-size mode from KINDI_Q4_VERIFY unless told
+(q4pack.py:80-84, gpu4.py:55).  ``PackWeights`` is the device side of gpu4.Weights
+(gpu4.py:17-48): ``w[name] -> (buf, R, C, type)`` with ``buf`` a device uint8 tensor in the Kindi
+layout, read with 8 MiB preads through two pinned staging buffers whose copies overlap the next
+read (large tensors by several reader threads over contiguous ranges), a least-recently used byte
+budget that spares the embedding and the head, and POSIX_FADV_DONTNEED after each tensor so the
+host page cache does not keep a second copy.  On a 288 GB MI355X the default budget
 keeps the whole 9B pack (5.6 GB) resident.  ``write_pack`` builds a pack from tensors already in
 the Kindi layout (the converter from GGUF, q4pack.convert, is not part of this path).
 """
+import concurrent.futures as cf
 import hashlib
 import json
 import os
@@ -216,18 +217,20 @@ class PackWeights:
         the reader's two pinned buffers, each copy to the device overlapping the next read."""
         stage, events = self._stage[t], self._events[t]
         stream = self._streams[t] or torch.cuda.current_stream(self.device)
-        with torch.cuda.stream(stream):
-            for i, off in enumerate(range(lo, hi, STAGE_BYTES)):
-                n = min(STAGE_BYTES, hi - off)
-                s, ev = stage[i % 2], events[i % 2]
-                ev.synchronize()                               # its previous copy has finished
-                view = memoryview(s.numpy())[:n]
-                if os.preadv(self.fd, [view], base + off) != n:
-                    raise IOError("Truncated Q4 weight tensor")
-                buf[off:off + n].copy_(s[:n], non_blocking=True)
-                ev.record(stream)
-        for ev in events:
-            ev.synchronize()
+        try:
+            with torch.cuda.stream(stream):
+                for i, off in enumerate(range(lo, hi, STAGE_BYTES)):
+                    n = min(STAGE_BYTES, hi - off)
+                    s, ev = stage[i % 2], events[i % 2]
+                    ev.synchronize()                           # its previous copy has finished
+                    view = memoryview(s.numpy())[:n]
+                    if os.preadv(self.fd, [view], base + off) != n:
+                        raise IOError("Truncated Q4 weight tensor")
+                    buf[off:off + n].copy_(s[:n], non_blocking=True)
+                    ev.record(stream)
+        finally:
+            for ev in events:                                  # no copy outlives the call, even on error
+                ev.synchronize()
         return hi - lo
 
     def _evict_for(self, size):
@@ -256,13 +259,15 @@ class PackWeights:
             # READERS contiguous ranges (whole staging chunks), read at once: the copies from the
             # page cache (or the device's queue depth) bound a single reader
             if self._pool is None:
-                import concurrent.futures as cf
                 self._pool = cf.ThreadPoolExecutor(READERS - 1)
             chunks = (size + STAGE_BYTES - 1) // STAGE_BYTES
             cut = [min(size, (chunks * t // READERS) * STAGE_BYTES) for t in range(READERS + 1)]
             futs = [self._pool.submit(self._read_range, t, buf, rec["offset"], cut[t], cut[t + 1])
                     for t in range(1, READERS)]
-            done = self._read_range(0, buf, rec["offset"], cut[0], cut[1])
+            try:
+                done = self._read_range(0, buf, rec["offset"], cut[0], cut[1])
+            finally:
+                cf.wait(futs)                                  # every reader has stopped writing into buf
             self.read_bytes += done + sum(f.result() for f in futs)
         os.posix_fadvise(self.fd, rec["offset"], rec["padded_bytes"], os.POSIX_FADV_DONTNEED)
         value = (buf, int(rec["rows"]), int(rec["ne0"]), int(rec["type"]))

@@ -83,6 +83,25 @@ def test_engine_rejects_bad_calls(layer, dev):
         eng.gemv_batch(["attn_q"], torch.zeros((17, 4096), device=dev), [torch.empty((17, 4096), device=dev)])
     with pytest.raises(KeyError):
         eng.gemv(["missing"], x, [torch.empty(4096, device=dev)])
+    with pytest.raises(ValueError, match="one output per matrix"):
+        eng.gemv_batch(["attn_q", "attn_k"], torch.zeros((2, 4096), device=dev), [torch.empty((2, 4096), device=dev)])
+    with pytest.raises(ValueError, match="one output per matrix"):
+        eng.gemm(["attn_q", "attn_k"], torch.zeros((2, 4096), device=dev), [torch.empty((2, 4096), device=dev)])
+
+
+def test_engine_batch_of_one_row_into_a_flat_output(layer, dev):
+    """gemv_batch and gemm with one row and a 1-D output (row stride R) equal gemv."""
+    w, _ = layer
+    eng = Engine(w, mode="q8k")
+    x = torch.from_numpy(kqq.synthetic_activations(1, 4096, seed=17)).to(dev)
+    ref = torch.empty(4096, device=dev)
+    eng.gemv(["attn_q"], x[0], [ref])
+    for fn in (eng.gemv_batch, eng.gemm):
+        y = torch.full((4096,), float("nan"), device=dev)
+        fn(["attn_q"], x, [y])
+        torch.cuda.synchronize()
+        err = (y - ref).abs().max().item()
+        assert err <= 1e-5 * ref.abs().max().item(), (fn.__name__, err)
 
 
 def test_dequant_row_matches_oracle(layer, orc, dev):

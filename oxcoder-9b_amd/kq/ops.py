@@ -22,6 +22,9 @@ def _dev(t, name, dtype=None):
         raise ValueError("%s must be a device tensor" % name)
     if dtype is not None and t.dtype != dtype:
         raise ValueError("%s must be %s, got %s" % (name, dtype, t.dtype))
+    if t.dim() > 0 and t.shape[-1] > 1 and t.stride(-1) != 1:
+        # kernels read consecutive elements of a row; rows may be strided (ld arguments)
+        raise ValueError("%s must have unit stride along its last dimension" % name)
     return C.c_void_p(t.data_ptr())
 
 

@@ -83,6 +83,10 @@ def test_engine_rejects_bad_calls(layer, dev):
         eng.gemv_batch(["attn_q"], torch.zeros((17, 4096), device=dev), [torch.empty((17, 4096), device=dev)])
     with pytest.raises(KeyError):
         eng.gemv(["missing"], x, [torch.empty(4096, device=dev)])
+    with pytest.raises(ValueError, match="unit stride|contiguous"):
+        eng.gemv(["attn_q"], torch.zeros(8192, device=dev)[::2], [torch.empty(4096, device=dev)])
+    with pytest.raises(ValueError, match="unit stride|contiguous"):
+        eng.gemv(["attn_q"], x, [torch.empty(8192, device=dev)[::2]])
     with pytest.raises(ValueError, match="one output per matrix"):
         eng.gemv_batch(["attn_q", "attn_k"], torch.zeros((2, 4096), device=dev), [torch.empty((2, 4096), device=dev)])
     with pytest.raises(ValueError, match="one output per matrix"):

@@ -517,6 +517,8 @@ def main():
                          "workload once per layer copy, then one 64 MiB device copy (the calibration "
                          "kernel); 'gemm' runs each prefill GEMM shape twice")
     a = ap.parse_args()
+    if a.steps < 1 or a.warmup < 0 or a.copies < 1:
+        ap.error("--steps and --copies must be positive, --warmup not negative")
     if a.gpus != 1:
         print("bench.py measures one GPU: the library has no multi-GPU path (the products would shard by "
               "output rows, with one all-reduce per token for o and down). Run with --gpus 1.", file=sys.stderr)
@@ -548,11 +550,19 @@ def main():
         return fn
 
     full = capture(torch, steps(a.copies))
-    rem = a.steps % a.copies
-    tail = capture(torch, steps(rem)) if rem else None
-    plan = [full] * (a.steps // a.copies) + ([tail] if tail else [])
+    graphs = {a.copies: full}
+
+    def plan_of(n):
+        # exactly n steps: whole graphs of `copies` steps, then one graph of the remainder
+        rem = n % a.copies
+        if rem and rem not in graphs:
+            graphs[rem] = capture(torch, steps(rem))
+        return [full] * (n // a.copies) + ([graphs[rem]] if rem else [])
+
+    plan = plan_of(a.steps)
     log("bench: warmup %d steps" % a.warmup)
-    time_graphs(torch, [full] * max(1, a.warmup // a.copies))
+    if a.warmup:
+        time_graphs(torch, plan_of(a.warmup))
     el = time_graphs(torch, plan)
     per_step = el / a.steps
     nbytes = step_bytes()

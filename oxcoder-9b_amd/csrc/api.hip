@@ -182,7 +182,7 @@ int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, fl
     KQ_TRY(check_ptr(xq, 4, "xq", fn));
     KQ_TRY(check_ptr(y, 4, "y", fn));
     launch_gemv_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), N, y,
-                    ldy, 0, as_stream(stream));
+                    ldy, as_stream(stream));
     return check_launch(fn);
 }
 

@@ -475,6 +475,9 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
 // share each pass's activations (4096x12288: 12.9 -> 12.3 us; one token: no difference).
 static int pick_rpw(int nt, int type, int G) {
 #ifdef KQ_GEMV_RPW
+#if KQ_GEMV_RPW != 1 && KQ_GEMV_RPW != 2
+#error "KQ_GEMV_RPW must be 1 or 2 (the launcher instantiates only these)"
+#endif
     (void)nt; (void)type; (void)G;
     return KQ_GEMV_RPW;
 #else
@@ -537,12 +540,8 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
 
 template <int TYPE, int NT>
 static void launch2(const MatGroup& mg, const uint8_t* xq, int G, int rpw, hipStream_t s) {
-    switch (rpw) {
-        case 1: launch3<TYPE, NT, 1>(mg, xq, G, s); break;
-        case 2: launch3<TYPE, NT, 2>(mg, xq, G, s); break;
-        case 4: launch3<TYPE, NT, 4>(mg, xq, G, s); break;
-        default: launch3<TYPE, NT, 8>(mg, xq, G, s); break;
-    }
+    if (rpw == 1) launch3<TYPE, NT, 1>(mg, xq, G, s);
+    else launch3<TYPE, NT, 2>(mg, xq, G, s);
 }
 
 template <int TYPE>
@@ -607,8 +606,7 @@ void launch_gemv_q8k_argmax(const uint8_t* w, int R, int C, int type, const uint
 }
 
 void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N, float* y,
-                     int64_t ldy, int rows_per_wave, hipStream_t s) {
-    (void)rows_per_wave;
+                     int64_t ldy, hipStream_t s) {
     launch_gemv_q8k_group(1, &w, &R, C, type, xq, N, &y, &ldy, s);
 }
 

@@ -32,7 +32,7 @@ void launch_rms_q8k(float* h, const float* res, int add, const float* w, int D, 
 void launch_swiglu_q8k(const float* gate, const float* up, int n, int N, int64_t ld, float* y, uint8_t* xq,
                        hipStream_t s);
 void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N, float* y,
-                     int64_t ldy, int rows_per_wave, hipStream_t s);
+                     int64_t ldy, hipStream_t s);
 // n (1..3) matrices of one type sharing xq; one launch per group of up to 4 tokens.
 void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s);

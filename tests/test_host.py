@@ -191,3 +191,21 @@ def test_missing_library_raises(monkeypatch):
         _lib.kq()
     with pytest.raises(RuntimeError, match="not built"):
         ops.gemm_workspace_bytes(4096, 4096, 512)
+
+
+@pytest.mark.parametrize("args,code,text", [
+    (["--gpus", "2"], 2, "measures one GPU"),
+    (["--gpus", "8"], 2, "measures one GPU"),
+    (["--steps", "0"], 2, "--steps and --copies must be positive"),
+    (["--warmup", "-1"], 2, "--warmup not negative"),
+])
+def test_bench_refuses_what_it_does_not_measure(args, code, text):
+    """bench.py exits before touching a GPU: more than one GPU (no multi-GPU path) or counts that
+    cannot be timed."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == code, (r.returncode, r.stderr)
+    assert text in r.stderr
+    assert r.stdout == ""

@@ -124,7 +124,9 @@ class Engine:
 
     def rmsfold_q8k(self, h, w, residual=None, xn=None):
         """h += residual (when given, in place), then RMSNorm(h) * w written as Q8_K into the engine
-        workspace (and to xn when given).  Returns (xn, xq) for gemv_q8."""
+        workspace (and to xn when given).  Returns (xn, xq) for gemv_q8.  xq is a view of the engine's
+        one Q8_K workspace (like the reference's reused xp scratch, gpu4.py:70-79): the next call that
+        quantizes (gemv in "q8k" mode, gemv_batch, gemm, head, rmsfold_q8k, swiglu_q8k) overwrites it."""
         N = 1 if h.dim() == 1 else h.shape[0]
         D = h.shape[-1]
         if D > self.max_cols or N > self.max_rows:
@@ -133,7 +135,7 @@ class Engine:
 
     def swiglu_q8k(self, gate, up, y=None):
         """silu(gate) * up written as Q8_K into the engine workspace (and to y when given).
-        Returns (y, xq) for gemv_q8."""
+        Returns (y, xq) for gemv_q8; xq is valid until the next quantizing call, as for rmsfold_q8k."""
         N = 1 if gate.dim() == 1 else gate.shape[0]
         n = gate.shape[-1]
         if n > self.max_cols or N > self.max_rows:

@@ -166,6 +166,23 @@ int kq_gemm_q8k_ws(const void* w, int R, int C, int type, const void* xq, int M,
                    int64_t ldy, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * kq_gemm_q8k_ws without a caller workspace and without any allocation: the workspace is the
+ * library's static device array of KQ_GEMM_STATIC_SCRATCH_BYTES (one per device, held until the
+ * process ends; a 256-token prefill chunk of every 9B-model matrix fits).  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Results are bit-identical to
+ * kq_gemm_q8k_ws on the same inputs.  A GEMM whose kq_gemm_q8k_workspace(R, C, M) exceeds the
+ * array is rejected with KQ_ERR_ARG before any launch.  The device address of the array is looked
+ * up on the first call on each device (the current device; `stream` must belong to it).  Calls on
+ * one device share the array: calls that overlap in time on one GPU (different streams, or
+ * different threads without ordering) race and give wrong results; calls ordered on one stream are
+ * safe.  Nothing in the array needs to start at zero: each call writes what it reads.
+ */
+#define KQ_GEMM_STATIC_SCRATCH_BYTES (32u << 20)
+int kq_gemm_q8k_static(const void* w, int R, int C, int type, const void* xq, int M, float* y,
+                       int64_t ldy, void* stream);
+
+/*
  * Exact integer sub-block sums, for parity checks:
  *   Q4_K: sums[((n*R + r)*G + g)*8 + s]  = sum_{j<32} q4 * q8 over sub-block s (q4 in 0..15)
  *   Q6_K: sums[((n*R + r)*G + g)*16 + t] = sum_{j<16} (q6 - 32) * q8 over sub-block t

@@ -255,6 +255,23 @@ int kq_gemm_q8k_ws(const void* w, int R, int C, int type, const void* xq, int M,
     return check_launch(fn);
 }
 
+int kq_gemm_q8k_static(const void* w, int R, int C, int type, const void* xq, int M, float* y,
+                       int64_t ldy, void* stream) {
+    static const char* fn = "kq_gemm_q8k_static";
+    KQ_TRY(check_gemm(w, R, C, type, xq, M, y, ldy, fn));
+    const size_t need = gemm_q8k_workspace(R, C, M);
+    if (need > KQ_GEMM_STATIC_SCRATCH_BYTES)
+        return fail(KQ_ERR_ARG,
+                    "%s: R=%d C=%d M=%d needs %zu bytes of workspace, more than the %u-byte static scratch "
+                    "(split M into chunks, or use kq_gemm_q8k_ws)", fn, R, C, M, need,
+                    (unsigned)KQ_GEMM_STATIC_SCRATCH_BYTES);
+    uint8_t* ws = nullptr;
+    KQ_TRY(gemm_static_scratch(&ws, fn));
+    launch_gemm_q8k(static_cast<const uint8_t*>(w), R, C, type, static_cast<const uint8_t*>(xq), M, y, ldy, ws,
+                    as_stream(stream));
+    return check_launch(fn);
+}
+
 int kq_subblock_sums(const void* w, int R, int C, int type, const void* xq, int N, int32_t* sums,
                      void* stream) {
     static const char* fn = "kq_subblock_sums";

@@ -41,6 +41,8 @@
 // S partial planes of the workspace; k_gemm_reduce then adds the planes in order s = 0, 1, ...
 // The split depends only on (R, C, M), so results are deterministic; it needs the workspace, so
 // kq_gemm_q8k (no workspace) never splits.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "kq_device.h"
@@ -549,6 +551,41 @@ static void launch_type(const uint8_t* w, int R, int G, const uint8_t* xq, const
     // the other's MFMAs.  (Measured against 128 x 128 tiles, one wave per SIMD, 4-8 waves per
     // workgroup: 289-317 against 331-379 us at M = 2048.)
     launch_tile<TYPE, 64, 2, 2>(w, R, G, xq, xf, M, y, ldy, S, gps, part, s);
+}
+
+// ------------------------------------------------------------------ the no-allocation form
+// Workspace of kq_gemm_q8k_static: a file-scope device array, one copy per device, held until the
+// process ends.  Its name is a host-side stand-in in host code; kernels get the device address that
+// hipGetSymbolAddress returns, looked up once per device (with that device current) on the first
+// call there.  Every call on a device shares that device's copy.
+static __device__ __align__(256) uint8_t scratch[KQ_GEMM_STATIC_SCRATCH_BYTES];
+
+constexpr int SCRATCH_DEVICES = 64;
+static std::atomic<uint8_t*> g_scratch[SCRATCH_DEVICES];
+static std::mutex g_scratch_mu;
+
+int gemm_static_scratch(uint8_t** out, const char* fn) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(KQ_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+    if (dev < 0 || dev >= SCRATCH_DEVICES)
+        return fail(KQ_ERR_ARG, "%s: device %d beyond the %d the library tracks", fn, dev, SCRATCH_DEVICES);
+    uint8_t* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            void* addr = nullptr;
+            const hipError_t r = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (r != hipSuccess || !addr)
+                return fail(KQ_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                            hipGetErrorString(r));
+            p = static_cast<uint8_t*>(addr);
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return KQ_OK;
 }
 
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,

@@ -44,6 +44,9 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
 size_t gemm_q8k_workspace(int R, int C, int M);
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
                      uint8_t* ws, hipStream_t s);
+// Device address of the static GEMM workspace on the current device (KQ_GEMM_STATIC_SCRATCH_BYTES),
+// looked up on the first call per device; fails with KQ_ERR_HIP when the lookup fails.
+int gemm_static_scratch(uint8_t** out, const char* fn);
 // Argmax (argmax_block.h): ws holds argmax_workspace_bytes() bytes, its first word zero.
 size_t argmax_workspace_bytes();
 void launch_argmax(const float* y, int n, uint8_t* ws, int* out, hipStream_t s);

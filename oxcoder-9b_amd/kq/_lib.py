@@ -30,6 +30,7 @@ KQ_SYMBOLS = {
     "kq_gemm_q8k": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),
     "kq_gemm_q8k_workspace": (C.c_size_t, [_i, _i, _i]),
     "kq_gemm_q8k_ws": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp, C.c_size_t, _vp]),
+    "kq_gemm_q8k_static": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),
     "kq_subblock_sums": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _vp]),
     "kq_dequant_rows": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _i64, _vp]),
 }
@@ -44,6 +45,7 @@ KQ_OK = 0
 KQ_ERR_ARG = -1
 KQ_ERR_HIP = -2
 KQ_MAX_BATCH = 16
+KQ_GEMM_STATIC_SCRATCH_BYTES = 32 << 20
 
 _libs = {}
 

@@ -183,6 +183,24 @@ def test_gemm_workspace_follows_the_split_rule():
         assert lib.kq_gemm_q8k_workspace(R, C, M) == 0, (R, C, M)
 
 
+def test_static_gemm_limit_checked_on_the_host():
+    """kq_gemm_q8k_static rejects a GEMM whose workspace exceeds its static array before touching a
+    device (host only); a 256-token chunk of every 9B-model matrix fits the array."""
+    from kq import _lib
+    lib = _lib.kq()
+    m = re.search(r"#define KQ_GEMM_STATIC_SCRATCH_BYTES \((\d+)u << (\d+)\)",
+                  open(os.path.join(ROOT, "include", "kq.h")).read())
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.KQ_GEMM_STATIC_SCRATCH_BYTES
+    for R, C in [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (8192, 4096)]:
+        assert lib.kq_gemm_q8k_workspace(R, C, 256) <= _lib.KQ_GEMM_STATIC_SCRATCH_BYTES, (R, C)
+    R, C, M = 4096, 12288, 4096
+    assert lib.kq_gemm_q8k_workspace(R, C, M) > _lib.KQ_GEMM_STATIC_SCRATCH_BYTES
+    p = ctypes.c_void_p(4096)
+    rc = lib.kq_gemm_q8k_static(p, R, C, 14, p, M, p, R, None)
+    assert rc == _lib.KQ_ERR_ARG
+    assert "static scratch" in lib.kq_last_error().decode()
+
+
 def test_missing_library_raises(monkeypatch):
     """No fallback: without the built library every entry point raises."""
     from kq import _lib, ops

@@ -13,7 +13,8 @@ value = algorithmic bytes per step (weights + activations read + outputs written
         / measured time per step, in GB/s.
 Also reported: the dominant kernel's roofline fraction (Q4_K GEMV, per-launch HIP events), the
 reference CPU path (kc_matvec, fp32 activations) on the host cores, speculative-verify batched
-GEMV, the prefill GEMM and the full decode weight stream.
+GEMV, the fp32-activation drop-in over the same layer, the prefill GEMM, the output heads and the
+full decode weight stream.
 """
 import argparse
 import ctypes as C
@@ -21,6 +22,7 @@ import json
 import os
 import sys
 import statistics
+import subprocess
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -209,14 +211,45 @@ def traffic_from_profile(path=os.path.join(ROOT, "profiles", "gemv_q4k_decode_la
     return None
 
 
+def host_cpus():
+    """CPUs this process can use, read from the host: the affinity mask (os.sched_getaffinity), the
+    cgroup CPU quota (/sys/fs/cgroup/cpu.max, cpu.cfs_quota_us) and lscpu's physical cores of the
+    whole machine.  ``usable`` = the affinity count, capped by the quota when there is one."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    for path, fmt in (("/sys/fs/cgroup/cpu.max", "v2"), ("/sys/fs/cgroup/cpu/cpu.cfs_quota_us", "v1")):
+        try:
+            if fmt == "v2":
+                q, period = open(path).read().split()[:2]
+                if q != "max":
+                    quota = int(q) / int(period)
+            else:
+                q = int(open(path).read())
+                period = int(open(os.path.join(os.path.dirname(path), "cpu.cfs_period_us")).read())
+                if q > 0:
+                    quota = q / period
+            break
+        except (OSError, ValueError):
+            continue
+    phys = None
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, timeout=20).stdout
+        phys = len({l for l in out.splitlines() if l and not l.startswith("#")}) or None
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    usable = aff if quota is None else max(1, min(aff, int(quota)))
+    return {"affinity": aff, "cgroup_quota": quota, "physical_cores_host": phys, "usable": usable}
+
+
 def cpu_baseline(budget_s=12.0, budget_2t_s=6.0, runs=5):
     """The reference's CPU path (kc_matvec, fp32 activations) on the same layer shapes: `runs` timed
-    runs after one warm-up, median, at the host's CPU share for one GPU (16 threads unless KQ_CPU_THREADS or
-    OMP_NUM_THREADS says otherwise) and at 2 threads (the reference's validated default,
-    scripts/kindi_q4/kindi/cpu4.py:99)."""
+    runs after one warm-up, median, on every CPU this process can use (host_cpus(): the affinity
+    mask capped by the cgroup quota; KQ_CPU_THREADS overrides) and on 2 threads (the reference's
+    validated default, scripts/kindi_q4/kindi/cpu4.py:99)."""
     from kq import quantize as kqq
     from oracle import oracle
-    threads = int(os.environ.get("KQ_CPU_THREADS", os.environ.get("OMP_NUM_THREADS", "16")))
+    hc = host_cpus()
+    threads = int(os.environ.get("KQ_CPU_THREADS", hc["usable"]))
     gomp = C.CDLL("libgomp.so.1")
     kind = "reference" if oracle.ref_available() else "port"
     mats = []
@@ -252,6 +285,9 @@ def cpu_baseline(budget_s=12.0, budget_2t_s=6.0, runs=5):
     v2, n2 = timed(2, budget_2t_s)
     gomp.omp_set_num_threads(threads)
     return {"value": round(v, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "cores_source": "KQ_CPU_THREADS" if "KQ_CPU_THREADS" in os.environ else
+                            "os.sched_getaffinity(0) capped by the cgroup CPU quota",
+            "host_cpus": hc,
             "value_2_threads": round(v2, 3),
             "sample": "median of %d runs (%d decode-layer steps in %.0f s) of the 7 matvecs of one decode layer "
                       "(fp32 activations, kc_matvec%s) rotating 4 host copies (486 MB); value_2_threads: the same, "
@@ -334,6 +370,31 @@ def producers_extra(torch, rn, layers, dev, steps=320):
     return out
 
 
+def f32_layer_extra(torch, rn, layers, dev, steps=320):
+    """The fp32-activation drop-in for q4_gemv (kq_gemv: Kindi's numerics, no activation
+    quantization) over one decode layer's 7 matrices, one launch per matrix as gpu4.Engine.gemv
+    launches q4_gemv (gpu4.py:95-99); the resident layer copies rotate, replayed from a graph.
+    Algorithmic bytes: weights + fp32 input (C*4) + fp32 output (R*4) per matrix."""
+    from kq import quantize as kqq
+    xs = [torch.from_numpy(kqq.synthetic_activations(1, c, seed=s)[0]).to(dev) for s, c in enumerate(INPUT_COLS)]
+    ys = {name: torch.empty(R, device=dev) for name, R, _, _, _ in LAYER}
+    p = lambda t: C.c_void_p(t.data_ptr())
+
+    def run_all():
+        s = rn.stream()
+        for lay in layers:
+            for name, R, C_, ty, slot in LAYER:
+                rn.check(rn.lib.kq_gemv(p(lay[name]), R, C_, ty, p(xs[slot]), p(ys[name]), s))
+
+    g = capture(torch, run_all)
+    time_graphs(torch, [g] * 2)
+    reps = max(1, steps // len(layers))
+    per = time_graphs(torch, [g] * reps) / (reps * len(layers))
+    nbytes = sum(wbytes(R, C_, ty) + C_ * 4 + R * 4 for _, R, C_, ty, _ in LAYER)
+    return {"layer_us": round(per * 1e6, 2), "bytes_per_layer": nbytes,
+            "GB/s": round(nbytes / per / 1e9, 1), "hbm_frac": round(nbytes / per / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def pack_extra(torch, dev, layers=2):
     """Pack loading (the F3 path, gpu4.Weights over a Kindi pack): write a pack with the 9B profile's
     dimensions for `layers` layers plus the 248320-row embedding and head (random block bytes: the
@@ -397,7 +458,8 @@ def pack_extra(torch, dev, layers=2):
 
 def head_extra(torch, rn, dev):
     """Output head 151936x4096 Q6_K with the greedy pick: fused (kq_gemv_q8k_argmax) against the GEMV
-    followed by kq_argmax; two resident copies (1 GB) alternate so the cache does not serve them."""
+    followed by kq_argmax; two resident copies (1 GB) alternate so the cache does not serve them.
+    Then a 248320x4096 Q4_K head (the real model's output size), GEMV and fused, two copies."""
     from kq import ops, quantize as kqq
     R, C_ = 151936, 4096
     w0 = torch.from_numpy(kqq.synthetic_matrix(R, C_, 14, seed=999)).to(dev)
@@ -426,6 +488,35 @@ def head_extra(torch, rn, dev):
         res[name] = round(time_graphs(torch, [g] * 10) / 20 * 1e6, 2)
     res["weight_GB/s_fused"] = round(wbytes(R, C_, 14) / (res["fused_us"] * 1e-6) / 1e9, 1)
     del ws_w, w0
+    # the real model's output size as Q4_K (output.weight 248320x4096, q4pack.py:22): random block
+    # bytes with fp16 scales of a N(0, 0.02) row; the Q4_K GEMV's rate where the launch cost is
+    # negligible (572 MB per launch)
+    R4 = 248320
+    rng = np.random.default_rng(5)
+    raw = rng.integers(0, 256, (R4 * 16, 144), dtype=np.uint8)
+    raw[:, 0:2] = np.array([4e-4], np.float16).view(np.uint8)
+    raw[:, 2:4] = np.array([1e-3], np.float16).view(np.uint8)
+    q0 = torch.from_numpy(raw.reshape(-1)).to(dev)
+    del raw
+    ws4 = [q0, q0.clone()]
+    y4 = torch.empty(R4, device=dev)
+
+    def gemv4():
+        for w in ws4:
+            rn.gemv(w, R4, C_, 12, xq, 1, y4, rn.stream())
+
+    def fused4():
+        for w in ws4:
+            rn.check(lib.kq_gemv_q8k_argmax(p(w), R4, C_, 12, p(xq), p(y4), p(aws), p(out), rn.stream()))
+
+    for name, fn in (("q4k_248320_gemv_us", gemv4), ("q4k_248320_fused_us", fused4)):
+        g = capture(torch, fn)
+        time_graphs(torch, [g] * 3)
+        res[name] = round(time_graphs(torch, [g] * 10) / 20 * 1e6, 2)
+    nb = wbytes(R4, C_, 12) + (C_ // 256) * Q8K + R4 * 4
+    res["q4k_248320_GB/s"] = round(nb / (res["q4k_248320_gemv_us"] * 1e-6) / 1e9, 1)
+    res["q4k_248320_hbm_frac"] = round(nb / (res["q4k_248320_gemv_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    del ws4, q0
     return res
 
 
@@ -583,6 +674,9 @@ def main():
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "traffic_source": "profiles/gemv_q4k_decode_layer_traffic.md: rocprofv3 --pmc FETCH_SIZE and "
+                                       "WRITE_SIZE of bench.py --pmc-workload gemv, calibrated on a 64 MiB copy "
+                                       "(read from that committed summary, not measured in this run)",
                      "kernel": "k_gemv_q8k_split<12,1,2> (Q4_K x Q8_K GEMV: q+k+v, o, gate+up launches)",
                      "launches": kn,
                      "avg_bytes_per_launch": round(kb), "avg_us_per_launch": round(ks * 1e6, 3)},
@@ -592,6 +686,8 @@ def main():
         result["batched_gemv"] = batched_extra(torch, rn, dev, 160)
         log("bench: fused producers")
         result["producers"] = producers_extra(torch, rn, layers, dev)
+        log("bench: fp32-activation layer")
+        result["f32_layer"] = f32_layer_extra(torch, rn, layers, dev)
         log("bench: prefill GEMM")
         result["prefill_gemm"] = gemm_extra(torch, rn, dev)
         del layers

@@ -25,9 +25,12 @@ runs the named matrices on that Q8_K input with no further quantization.  ``head
 head with the greedy pick (Engine.head, engine.py:323-331): the GEMV computes the argmax of the
 logits as it stores them (kq_gemv_q8k_argmax).
 """
+import os
+
 import torch
 
 from . import ops
+from ._lib import KQ_MAX_BATCH
 from .formats import BLOCK, Q8K_BYTES, QK, check_shape
 
 
@@ -52,29 +55,65 @@ class Weights:
         return name in self.cache
 
 
-def _widest(weights):
-    """Most columns of any quantized tensor the weights hold: from the pack index when there is
-    one (a PackWeights reads tensors lazily, so its cache starts empty), else from the resident
-    tensors."""
+def _tensor_shapes(weights):
+    """(R, C) of every quantized tensor the weights hold: from the pack index when there is one (a
+    PackWeights reads tensors lazily, so its cache starts empty), else from the resident tensors."""
     index = getattr(weights, "index", None)
     if index is not None:
-        return max([r["ne0"] for r in index.values() if r["type"] in BLOCK] or [QK])
-    return max([C for (_, _, C, _) in weights.cache.values()] or [QK])
+        return sorted({(int(r["rows"]), int(r["ne0"])) for r in index.values() if r["type"] in BLOCK})
+    return sorted({(R, C) for (_, R, C, _) in weights.cache.values()})
+
+
+def chunk_from_env():
+    """Tokens per prefill GEMM call, KINDI_CHUNK as the reference's chunked prefill reads it
+    (chunk.py:82,90: default 256; "0", "" or "1" turn chunked prefill off, and prompts then go
+    through the batched GEMV, 16 rows at a time)."""
+    v = os.environ.get("KINDI_CHUNK", "256")
+    if v in ("0", "", "1"):
+        return 0
+    n = int(v)
+    if n < 2:
+        raise ValueError("KINDI_CHUNK must be a positive token count")
+    return n
 
 
 class Engine:
-    def __init__(self, weights, mode="q8k", max_cols=None, max_rows=16):
+    """Every buffer a call uses is allocated here, as the reference engine preallocates its device
+    scratch (gpu4.py:70-79): the Q8_K activations of up to max(chunk, 16) rows, the prefill GEMM
+    workspace for any chunk of up to ``chunk`` rows of any of the weights' matrices, the argmax
+    workspace and the logits (as many as the tallest matrix has rows).  No call allocates device
+    memory, so any call can be captured into a HIP graph, the first one included."""
+
+    def __init__(self, weights, mode="q8k", max_cols=None, chunk=None, batch_max=KQ_MAX_BATCH):
         if mode not in ("q8k", "f32"):
             raise ValueError("mode must be 'q8k' or 'f32'")
+        if not 1 <= batch_max <= KQ_MAX_BATCH:
+            raise ValueError("batch_max must be 1..%d" % KQ_MAX_BATCH)
         self.w = weights
         self.mode = mode
         self.device = weights.device
-        cols = max_cols or _widest(weights)
+        shapes = _tensor_shapes(weights)
+        cols = max_cols or max([C for _, C in shapes] or [QK])
         self.max_cols = cols
-        self.max_rows = max_rows
-        # Q8_K workspace, preallocated like the reference's device scratch (gpu4.py:70-79).
-        self.xq = torch.empty(max_rows * (cols // QK) * Q8K_BYTES, dtype=torch.uint8, device=self.device)
-        self.gemm_ws = None   # prefill GEMM workspace (activation fragments, K-split partial sums), grown on demand
+        self.chunk = chunk_from_env() if chunk is None else int(chunk)
+        if self.chunk < 0 or self.chunk == 1:
+            raise ValueError("chunk must be 0 (no prefill GEMM) or at least 2 tokens")
+        self.batch_max = batch_max
+        self.max_rows = max(self.chunk, KQ_MAX_BATCH)
+        dev = self.device
+        # Q8_K workspace (the reference's reused xp scratch, gpu4.py:70-79)
+        self.xq = torch.empty(self.max_rows * (cols // QK) * Q8K_BYTES, dtype=torch.uint8, device=dev)
+        # prefill GEMM workspace: the most any chunk (1..chunk rows) of any matrix needs
+        need = 0
+        if self.chunk:
+            for R, C in shapes:
+                if C <= cols:
+                    need = max(need, max(ops.gemm_workspace_bytes(R, C, m) for m in range(1, self.chunk + 1)))
+        self.gemm_ws = torch.empty(need + 256, dtype=torch.uint8, device=dev) if need else None
+        self.argmax_ws = ops.argmax_workspace(dev)
+        self.argmax_out = torch.empty(1, dtype=torch.int32, device=dev)
+        self.logits = torch.empty(max([R for R, _ in shapes] or [1]), dtype=torch.float32, device=dev)
+        self.row = torch.empty(cols, dtype=torch.float32, device=dev)     # embed / dequant output
 
     def _check_out(self, y, R, N=1):
         need = (N - 1) * (y.stride(0) if y.dim() == 2 else R) + R
@@ -87,10 +126,16 @@ class Engine:
             raise ValueError("input %dx%d exceeds the engine workspace %dx%d" % (N, C, self.max_rows, self.max_cols))
         return ops.q8k_quantize(X, self.xq[: N * (C // QK) * Q8K_BYTES].view(N, -1))
 
-    def gemv(self, names, x, outs, parts_ok=False):
+    def _mats(self, names, outs):
+        """The named matrices and one output each (extra outputs are ignored, as zip does in the
+        reference's gemv, gpu4.py:96)."""
         mats = [self.w[n] for n in names]
         if len(outs) < len(mats):
             raise ValueError("one output per matrix")
+        return mats, list(outs)[:len(mats)]
+
+    def gemv(self, names, x, outs, parts_ok=False):
+        mats, outs = self._mats(names, outs)
         C = mats[0][2]
         if any(m[2] != C for m in mats) or x.numel() < C:
             raise ValueError("matrices sharing x must have the same column count")
@@ -103,14 +148,12 @@ class Engine:
         xq = self._quantize(x.reshape(1, -1)[:, :C], C)
         # matrices sharing the input go three at a time into one launch (kcpu4.c:100-118)
         for i in range(0, len(mats), 3):
-            ops.gemv_q8k_multi(mats[i:i + 3], xq, 1, list(outs[i:i + 3]))
+            ops.gemv_q8k_multi(mats[i:i + 3], xq, 1, outs[i:i + 3])
         return 1
 
     def gemv_q8(self, names, xq, outs, N=1):
         """gemv on an activation already in Q8_K (from rmsfold_q8k / swiglu_q8k); returns 1."""
-        mats = [self.w[n] for n in names]
-        if len(outs) < len(mats):
-            raise ValueError("one output per matrix")
+        mats, outs = self._mats(names, outs)
         C = mats[0][2]
         if any(m[2] != C for m in mats):
             raise ValueError("matrices sharing xq must have the same column count")
@@ -119,14 +162,15 @@ class Engine:
         for (w, R, _, _), y in zip(mats, outs):
             self._check_out(y, R, N)
         for i in range(0, len(mats), 3):
-            ops.gemv_q8k_multi(mats[i:i + 3], xq, N, list(outs[i:i + 3]))
+            ops.gemv_q8k_multi(mats[i:i + 3], xq, N, outs[i:i + 3])
         return 1
 
     def rmsfold_q8k(self, h, w, residual=None, xn=None):
         """h += residual (when given, in place), then RMSNorm(h) * w written as Q8_K into the engine
         workspace (and to xn when given).  Returns (xn, xq) for gemv_q8.  xq is a view of the engine's
         one Q8_K workspace (like the reference's reused xp scratch, gpu4.py:70-79): the next call that
-        quantizes (gemv in "q8k" mode, gemv_batch, gemm, head, rmsfold_q8k, swiglu_q8k) overwrites it."""
+        quantizes (gemv in "q8k" mode, gemv_batch, gemm, feed_rows, head, rmsfold_q8k, swiglu_q8k)
+        overwrites it."""
         N = 1 if h.dim() == 1 else h.shape[0]
         D = h.shape[-1]
         if D > self.max_cols or N > self.max_rows:
@@ -143,33 +187,38 @@ class Engine:
         return ops.swiglu_q8k(gate, up, y=y, xq=self.xq[: N * (n // QK) * Q8K_BYTES].view(N, -1))
 
     def head(self, name, x, y=None):
-        """Greedy next token: y = W_name x (the logits, kept in ``y`` or the engine's buffer) and the
-        index of the largest logit, read back to the host as Engine.head does (engine.py:323-331,
-        gemv + k_argmax); the GEMV finds the argmax itself (kq_gemv_q8k_argmax)."""
+        """Greedy next token: y = W_name x (the logits, kept in ``y`` or the engine's preallocated
+        buffer) and the index of the largest logit, read back to the host as Engine.head does
+        (engine.py:323-331, gemv + k_argmax); the GEMV finds the argmax itself (kq_gemv_q8k_argmax)."""
         w, R, C, ty = self.w[name]
         if self.mode != "q8k":
             raise ValueError("head: the fused greedy pick runs on Q8_K activations (mode 'q8k')")
         if y is None:
-            if getattr(self, "logits", None) is None or self.logits.numel() < R:
-                self.logits = torch.empty(R, dtype=torch.float32, device=self.device)
+            if self.logits.numel() < R:
+                raise ValueError("head: %d logits, the engine holds %d" % (R, self.logits.numel()))
             y = self.logits[:R]
         self._check_out(y, R)
-        if getattr(self, "argmax_ws", None) is None:
-            self.argmax_ws = ops.argmax_workspace(self.device)
-            self.argmax_out = torch.empty(1, dtype=torch.int32, device=self.device)
         xq = self._quantize(x.reshape(1, -1)[:, :C], C)
         ops.gemv_q8k_argmax(w, R, C, ty, xq, y, self.argmax_ws, self.argmax_out)
         return int(self.argmax_out.cpu()[0])
 
-    def feed_rows(self, names, X, outs, batch_max=16):
+    def feed_rows(self, names, X, outs, batch_max=None):
         """Several activation rows through the named matrices, as the engine's batched prompt and
-        verify paths need (Runner batching, cache.py:587-600; chunk.feed, chunk.py:378): up to
-        ``batch_max`` rows go through the batched GEMV, whose rows are bit-identical to one-token
-        decode (so a verified draft continues exactly as decode would), more rows through the
-        prefill GEMM."""
+        verify paths need (Runner batching up to batch_max rows, cache.py:587-600; chunked prefill,
+        chunk.py:165-177,378): up to ``batch_max`` rows (16 by default) go through the batched GEMV,
+        whose rows are bit-identical to one-token decode (a verified draft continues exactly as
+        decode would); more rows through the prefill GEMM in chunks of ``chunk`` tokens, or, with
+        chunked prefill off (chunk 0), through the batched GEMV 16 rows at a time."""
         N = X.shape[0]
-        if N <= batch_max:
+        bm = self.batch_max if batch_max is None else batch_max
+        if N <= bm:
             return self.gemv_batch(names, X, outs)
+        if not self.chunk:
+            mats, outs = self._mats(names, outs)
+            for n0 in range(0, N, KQ_MAX_BATCH):
+                n1 = min(N, n0 + KQ_MAX_BATCH)
+                self.gemv_batch(names, X[n0:n1], [y[n0:n1] for y in outs])
+            return 1
         return self.gemm(names, X, outs)
 
     def fingerprint(self):
@@ -182,34 +231,39 @@ class Engine:
     def gemv_batch(self, names, X, outs):
         """Speculative-verify GEMV: X [N][C], N <= 16; out[n][r] bit-identical to gemv on row n."""
         N, C = X.shape
-        if not 1 <= N <= 16:
-            raise ValueError("batch of %d rows: 1..16 supported" % N)
-        if len(outs) < len(names):
-            raise ValueError("one output per matrix")
-        xq = self._quantize(X, C)
-        for name, y in zip(names, outs):
-            w, R, C_, ty = self.w[name]
+        if not 1 <= N <= KQ_MAX_BATCH:
+            raise ValueError("batch of %d rows: 1..%d supported" % (N, KQ_MAX_BATCH))
+        mats, outs = self._mats(names, outs)
+        for (w, R, C_, ty), y in zip(mats, outs):
             if C_ != C:
-                raise ValueError("column count mismatch for " + name)
+                raise ValueError("column count mismatch")
             self._check_out(y, R, N)
+        xq = self._quantize(X, C)
+        for (w, R, C_, ty), y in zip(mats, outs):
             ops.gemv_q8k(w, R, C_, ty, xq, N, y, y.stride(0) if y.dim() == 2 else R)
         return 1
 
     def gemm(self, names, X, outs):
-        """Prefill GEMM over M rows of X [M][C] (M <= max_rows of the engine workspace)."""
+        """Prefill GEMM over any number M of rows of X [M][C], in chunks of ``chunk`` tokens as the
+        reference's chunked prefill feeds them (chunk.py:165-177,378): each chunk is quantized once
+        into the engine's Q8_K workspace, then every named matrix runs the GEMM on it with the
+        engine's GEMM workspace (kq_gemm_q8k_ws).  Chunk results equal one kq_gemm_q8k_ws call on
+        that chunk bit for bit.  Allocates nothing."""
         M, C = X.shape
-        if len(outs) < len(names):
-            raise ValueError("one output per matrix")
-        xq = self._quantize(X, C)
-        need = max(ops.gemm_workspace_bytes(self.w[name][1], C, M) for name in names) + 256
-        if self.gemm_ws is None or self.gemm_ws.numel() < need:
-            self.gemm_ws = torch.empty(need, dtype=torch.uint8, device=self.device)
-        for name, y in zip(names, outs):
-            w, R, C_, ty = self.w[name]
+        if not self.chunk:
+            raise ValueError("chunked prefill is off (chunk 0): use feed_rows or gemv_batch")
+        mats, outs = self._mats(names, outs)
+        for (w, R, C_, ty), y in zip(mats, outs):
             if C_ != C:
-                raise ValueError("column count mismatch for " + name)
+                raise ValueError("column count mismatch")
             self._check_out(y, R, M)
-            ops.gemm_q8k(w, R, C_, ty, xq, M, y, y.stride(0) if y.dim() == 2 else R, ws=self.gemm_ws)
+        for m0 in range(0, M, self.chunk):
+            mc = min(self.chunk, M - m0)
+            xq = self._quantize(X[m0:m0 + mc], C)
+            for (w, R, C_, ty), y in zip(mats, outs):
+                ldy = y.stride(0) if y.dim() == 2 else R     # a flat output holds rows of R
+                yv = y[m0:m0 + mc] if y.dim() == 2 else y[m0 * R:]
+                ops.gemm_q8k(w, R, C_, ty, xq, mc, yv, ldy, ws=self.gemm_ws)
         return 1
 
     def embed(self, tok, out=None, name="token_embd.weight"):
@@ -221,8 +275,15 @@ class Engine:
         return self.dequant(name, tok, out)
 
     def dequant(self, name, row, out=None):
-        """One decoded row (kc_dequant, kcpu4.c:341; q4_embed, q4.cu:28-32)."""
+        """One decoded row (kc_dequant, kcpu4.c:341; q4_embed, q4.cu:28-32) into ``out`` or the
+        engine's preallocated row buffer (the reference decodes the embedding into its h scratch,
+        gpu4.py:100-103), which the next embed/dequant call overwrites."""
         w, R, C, ty = self.w[name]
         if not 0 <= row < R:
             raise ValueError("Invalid row")
-        return ops.dequant_rows(w, R, C, ty, row, 1, out)[0] if out is None else ops.dequant_rows(w, R, C, ty, row, 1, out)
+        if out is None:
+            if C > self.row.numel():
+                raise ValueError("row of %d values, the engine holds %d" % (C, self.row.numel()))
+            out = self.row[:C]
+        ops.dequant_rows(w, R, C, ty, row, 1, out)
+        return out

@@ -239,6 +239,9 @@ def dequant_rows(w, R, C_, ty, row0, nrows, y=None):
     pw = _weights(w, R, C_, ty)
     if y is None:
         y = torch.empty((nrows, C_), dtype=torch.float32, device=w.device)
-    _lib.check(_lib.kq().kq_dequant_rows(pw, R, C_, ty, row0, nrows, _dev(y, "y", torch.float32),
-                                         y.stride(0) if y.dim() == 2 else C_, _stream(w.device)))
+    ld = y.stride(0) if y.dim() == 2 else C_
+    if y.numel() < (nrows - 1) * ld + C_:
+        raise ValueError("y holds %d floats, %d rows of %d need %d" % (y.numel(), nrows, C_, (nrows - 1) * ld + C_))
+    _lib.check(_lib.kq().kq_dequant_rows(pw, R, C_, ty, row0, nrows, _dev(y, "y", torch.float32), ld,
+                                         _stream(w.device)))
     return y

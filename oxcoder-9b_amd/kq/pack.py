@@ -260,6 +260,11 @@ class PackWeights:
             # page cache (or the device's queue depth) bound a single reader
             if self._pool is None:
                 self._pool = cf.ThreadPoolExecutor(READERS - 1)
+            # buf may reuse memory freed on the caller's stream (an evicted tensor) that kernels
+            # queued there still read: the readers' own copy streams start after them
+            cur = torch.cuda.current_stream(self.device)
+            for st in self._streams[1:]:
+                st.wait_stream(cur)
             chunks = (size + STAGE_BYTES - 1) // STAGE_BYTES
             cut = [min(size, (chunks * t // READERS) * STAGE_BYTES) for t in range(READERS + 1)]
             futs = [self._pool.submit(self._read_range, t, buf, rec["offset"], cut[t], cut[t + 1])

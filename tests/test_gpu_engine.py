@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from kq import quantize as kqq
+from kq import ops, quantize as kqq
 from kq.gpu4 import Engine, Weights
 
 pytestmark = pytest.mark.gpu
@@ -169,7 +169,7 @@ def test_engine_feed_rows_dispatch(layer, dev):
     """feed_rows: up to 16 rows through the batched GEMV (rows equal one-token decode bit for bit),
     more through the GEMM (same values within the GEMM's own bar, bit-equal to Engine.gemm)."""
     w, host = layer
-    eng = Engine(w, mode="q8k", max_rows=64)
+    eng = Engine(w, mode="q8k")
     X = torch.from_numpy(kqq.synthetic_activations(40, 4096, seed=9)).to(dev)
     names = ["ffn_gate"]
     y5 = torch.empty((5, 12288), device=dev)
@@ -192,7 +192,7 @@ def test_engine_prefill_gemm_split_k_layer(layer, dev):
     workspace: q/k/v (grids of 64 and 16 tiles: K split 4 ways) and down (K split 8 ways).  Every
     row is within the bar of its one-token GEMV, and a second call gives the same bits."""
     w, _ = layer
-    eng = Engine(w, mode="q8k", max_rows=64)
+    eng = Engine(w, mode="q8k")
     M = 48
     for names, C in ((["attn_q", "attn_k", "attn_v"], 4096), (["ffn_down"], 12288)):
         X = torch.from_numpy(kqq.synthetic_activations(M, C, seed=C + 3)).to(dev)
@@ -209,3 +209,114 @@ def test_engine_prefill_gemm_split_k_layer(layer, dev):
                 got = y[r0:r0 + 16].cpu().numpy()
                 assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max(), (n, r0)
             assert torch.equal(y, y2), n
+
+
+def test_engine_default_prefill_chunks(layer, dev, monkeypatch):
+    """A 300-token prompt through a default-constructed Engine (KINDI_CHUNK unset: chunks of 256
+    tokens, chunk.py:82,90): the rows of each chunk equal one kq_gemm_q8k_ws call on that chunk bit
+    for bit, for matrices that do and do not split K."""
+    monkeypatch.delenv("KINDI_CHUNK", raising=False)
+    w, _ = layer
+    eng = Engine(w)
+    assert eng.chunk == 256
+    M = 300
+    for names, C in ((["attn_q", "attn_k", "attn_v"], 4096), (["ffn_gate", "ffn_up"], 4096), (["ffn_down"], 12288)):
+        X = torch.from_numpy(kqq.synthetic_activations(M, C, seed=C + 11)).to(dev)
+        outs = [torch.empty((M, w[n][1]), device=dev) for n in names]
+        assert eng.gemm(names, X, outs) == 1
+        for n, y in zip(names, outs):
+            wt, R, C_, ty = w[n]
+            for m0, mc in ((0, 256), (256, 44)):
+                xq = ops.q8k_quantize(X[m0:m0 + mc])
+                ref = torch.empty((mc, R), device=dev)
+                ops.gemm_q8k(wt, R, C_, ty, xq, mc, ref, ws=ops.gemm_workspace(R, C_, mc, dev))
+                assert torch.equal(y[m0:m0 + mc], ref), (n, m0)
+
+
+@pytest.mark.parametrize("name,N", [("ffn_gate", 17), ("attn_q", 300)])
+def test_engine_feed_rows_long_inputs(layer, dev, orc, name, N):
+    """feed_rows on a default Engine with more rows than a batch (17) and more than a chunk (300)
+    against the oracle."""
+    w, host = layer
+    eng = Engine(w)
+    W, R, C, ty = host[name]
+    X = kqq.synthetic_activations(N, C, seed=N)
+    y = torch.empty((N, R), device=dev)
+    assert eng.feed_rows([name], torch.from_numpy(X).to(dev), [y]) == 1
+    torch.cuda.synchronize()
+    want = orc.gemv_q8k(W, R, C, ty, orc.quantize_q8k(X), N)
+    got = y.cpu().numpy()
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+
+
+def test_engine_feed_rows_without_chunked_prefill(layer, dev, monkeypatch):
+    """KINDI_CHUNK=0: no GEMM; longer inputs go through the batched GEMV 16 rows at a time, every
+    row bit-identical to one-token decode."""
+    monkeypatch.setenv("KINDI_CHUNK", "0")
+    w, _ = layer
+    eng = Engine(w)
+    assert eng.chunk == 0 and eng.gemm_ws is None
+    X = torch.from_numpy(kqq.synthetic_activations(37, 4096, seed=4)).to(dev)
+    y = torch.empty((37, 1024), device=dev)
+    eng.feed_rows(["attn_k"], X, [y])
+    for n in (0, 16, 36):
+        one = torch.empty(1024, device=dev)
+        eng.gemv(["attn_k"], X[n], [one])
+        assert torch.equal(y[n], one), n
+    with pytest.raises(ValueError, match="chunked prefill is off"):
+        eng.gemm(["attn_k"], X, [y])
+
+
+@pytest.mark.parametrize("mode", ["q8k", "f32"])
+def test_engine_gemv_ignores_extra_outputs(layer, dev, mode):
+    """More outputs than names: the extra ones are left alone, as the reference's zip does."""
+    w, _ = layer
+    eng = Engine(w, mode=mode)
+    x = torch.from_numpy(kqq.synthetic_activations(1, 4096, seed=8)[0]).to(dev)
+    outs = [torch.empty(4096, device=dev), torch.empty(1024, device=dev), torch.full((7,), -1.0, device=dev)]
+    assert eng.gemv(["attn_q", "attn_k"], x, outs) == 1
+    ref = [torch.empty(4096, device=dev), torch.empty(1024, device=dev)]
+    eng.gemv(["attn_q", "attn_k"], x, ref)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], ref[0]) and torch.equal(outs[1], ref[1])
+    assert torch.all(outs[2] == -1.0)
+
+
+def test_engine_first_calls_capture_into_a_graph(layer, dev):
+    """Nothing in an Engine call allocates, so a fresh Engine's first calls can be captured into a
+    HIP graph: a 300-token prefill of the down projection (two chunks, K split), a decode GEMV of
+    q/k/v and the token embedding.  Three replays, with eager calls of the same engine (which
+    overwrite its Q8_K workspace) between them, each equal bit for bit to the eager results."""
+    w, _ = layer
+    eng = Engine(w)
+    X = torch.from_numpy(kqq.synthetic_activations(300, 12288, seed=5)).to(dev)
+    x = torch.from_numpy(kqq.synthetic_activations(1, 4096, seed=6)[0]).to(dev)
+    qkv = ["attn_q", "attn_k", "attn_v"]
+
+    def outputs():
+        return [torch.full((300, 4096), float("nan"), device=dev)] + \
+               [torch.full((R,), float("nan"), device=dev) for R in (4096, 1024, 1024)] + \
+               [torch.full((4096,), float("nan"), device=dev)]      # one decoded row of ffn_gate
+
+    cap = outputs()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):                         # the engine's first calls
+        eng.gemm(["ffn_down"], X, [cap[0]])
+        eng.gemv(qkv, x, cap[1:4])
+        eng.dequant("ffn_gate", 77, cap[4])
+    ref = outputs()
+    eng.gemm(["ffn_down"], X, [ref[0]])
+    eng.gemv(qkv, x, ref[1:4])
+    eng.dequant("ffn_gate", 77, ref[4])
+    torch.cuda.synchronize()
+    other = torch.empty(12288, device=dev)
+    for rep in range(3):
+        for t in cap:
+            t.fill_(float("nan"))
+        eng.gemv(["ffn_gate"], X[rep, :4096], [other])   # eager work on the same workspace
+        g.replay()
+        eng.gemv(["ffn_up"], X[rep + 1, :4096], [other])
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(cap, ref)):
+            assert torch.equal(a, b), (rep, i)

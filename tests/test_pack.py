@@ -180,12 +180,74 @@ def test_engine_over_a_pack_sizes_its_workspace_from_the_index(tiny_pack):
     """A PackWeights reads tensors lazily (its cache starts empty), so the Engine takes the widest
     quantized tensor from the pack index: 512 columns (ffn_down) in the tiny pack.  No device
     work: the engine's workspace is a host tensor here."""
+    from kq import ops
     from kq.gpu4 import Engine
     w = pack.PackWeights(tiny_pack, device="cpu")
     try:
         assert len(w.cache) == 0
         eng = Engine(w, mode="q8k")
         assert eng.max_cols == 512
-        assert eng.xq.numel() == 16 * (512 // 256) * 292
+        assert eng.chunk == 256 and eng.xq.numel() == 256 * (512 // 256) * 292
+        # the GEMM workspace covers any chunk of 1..256 rows of every quantized tensor of the pack
+        need = max(ops.gemm_workspace_bytes(R, C, m) for R, C in [(16, 256), (8, 512)] for m in range(1, 257))
+        assert eng.gemm_ws.numel() == need + 256
+        assert eng.logits.numel() == 16 and eng.row.numel() == 512
+    finally:
+        w.close()
+
+
+@pytest.mark.parametrize("value,chunk", [(None, 256), ("128", 128), ("0", 0), ("1", 0), ("", 0)])
+def test_engine_chunk_follows_kindi_chunk(tiny_pack, monkeypatch, value, chunk):
+    """The prefill chunk is KINDI_CHUNK (chunk.py:82,90: default 256; 0, 1 or empty turn chunked
+    prefill off); with it off the engine keeps no GEMM workspace.  Host only."""
+    from kq.gpu4 import Engine
+    if value is None:
+        monkeypatch.delenv("KINDI_CHUNK", raising=False)
+    else:
+        monkeypatch.setenv("KINDI_CHUNK", value)
+    w = pack.PackWeights(tiny_pack, device="cpu")
+    try:
+        eng = Engine(w, mode="q8k")
+        assert eng.chunk == chunk
+        assert (eng.gemm_ws is None) == (chunk == 0)
+        assert eng.max_rows == max(chunk, 16)
+    finally:
+        w.close()
+
+
+def test_side_readers_wait_for_the_callers_stream(tiny_pack, monkeypatch):
+    """A large tensor is read by several threads, each copying on its own stream.  Before any reader
+    starts, those streams are made to wait for the caller's stream: the new device buffer may reuse
+    memory freed there (an evicted tensor) that queued kernels still read.  Host only: the streams
+    and the reads are stand-ins that record the order of events."""
+    import torch
+    events = []
+
+    class Stream:
+        def __init__(self, name):
+            self.name = name
+
+        def wait_stream(self, other):
+            events.append(("wait", self.name, other.name))
+
+    caller = Stream("caller")
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: caller)
+    monkeypatch.setattr(pack, "PARALLEL_MIN", 0)
+    w = pack.PackWeights(tiny_pack, device="cpu")
+    try:
+        w._stage, w._events = [], []                 # staging set up (not used by the stand-in reads)
+        w._streams = [None] + [Stream("s%d" % t) for t in range(1, pack.READERS)]
+
+        def read(t, buf, base, lo, hi):
+            events.append(("read", t))
+            return hi - lo
+
+        monkeypatch.setattr(w, "_read_range", read)
+        buf = w["token_embd.weight"][0]
+        assert buf.numel() == 16 * 144
+        waits = [e for e in events if e[0] == "wait"]
+        assert sorted(waits) == [("wait", "s%d" % t, "caller") for t in range(1, pack.READERS)]
+        first_read = min(i for i, e in enumerate(events) if e[0] == "read")
+        assert all(i < first_read for i, e in enumerate(events) if e[0] == "wait")
     finally:
         w.close()

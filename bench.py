@@ -199,6 +199,39 @@ def pmc_workload(torch, rn, layers, xs, xqs, ys, dev):
     log("pmc workload: %d GEMV launches, one 64 MiB copy" % (len(layers) * len(roofline_groups())))
 
 
+def pmc_workload_q6k(torch, rn, dev):
+    """Q6_K GEMV launches for counter runs (direct, no graph): the 151936x4096 output head and the
+    4096x12288 ffn_down, 4 calls each on alternating resident copies, then the 248320x4096 Q4_K
+    head twice for comparison, then a 64 MiB device copy (counter calibration)."""
+    from kq import ops, quantize as kqq
+    s = rn.stream()
+    for R, C_, ty, seed in ((151936, 4096, 14, 999), (4096, 12288, 14, 6)):
+        w0 = torch.from_numpy(kqq.synthetic_matrix(R, C_, ty, seed=seed)).to(dev)
+        ws = [w0, w0.clone()]
+        xq = ops.q8k_quantize(torch.from_numpy(kqq.synthetic_activations(1, C_, seed=0)).to(dev))
+        y = torch.empty(R, device=dev)
+        torch.cuda.synchronize()
+        for i in range(4):
+            rn.gemv(ws[i % 2], R, C_, ty, xq, 1, y, s)
+        torch.cuda.synchronize()
+        del ws, w0
+    R4, C4 = 248320, 4096
+    raw = np.random.default_rng(5).integers(0, 256, (R4 * 16, 144), dtype=np.uint8)
+    raw[:, 0:2] = np.array([4e-4], np.float16).view(np.uint8)
+    raw[:, 2:4] = np.array([1e-3], np.float16).view(np.uint8)
+    w4 = torch.from_numpy(raw.reshape(-1)).to(dev)
+    xq = ops.q8k_quantize(torch.from_numpy(kqq.synthetic_activations(1, C4, seed=0)).to(dev))
+    y = torch.empty(R4, device=dev)
+    for _ in range(2):
+        rn.gemv(w4, R4, C4, 12, xq, 1, y, s)
+    src = torch.ones(1 << 24, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log("pmc workload: Q6_K head x4, Q6_K down x4, Q4_K head x2, one 64 MiB copy")
+
+
 def traffic_from_profile(path=os.path.join(ROOT, "profiles", "gemv_q4k_decode_layer_traffic.md")):
     """HBM bytes per launch of the roofline kernel as recorded by the committed counter summary
     (line 'traffic_bytes_per_launch = N'), or None when the summary is absent."""
@@ -456,6 +489,15 @@ def pack_extra(torch, dev, layers=2):
         shutil.rmtree(root, ignore_errors=True)
 
 
+def warm_then_time(torch, g, launches, warm_s=0.1, reps=4):
+    """Replay graph g for at least warm_s seconds (clocks settle under sustained load), then time
+    `reps` replays; returns seconds per launch (g holds `launches` launches)."""
+    warm = 0.0
+    while warm < warm_s:
+        warm += time_graphs(torch, [g] * 2)
+    return time_graphs(torch, [g] * reps) / (reps * launches)
+
+
 def head_extra(torch, rn, dev):
     """Output head 151936x4096 Q6_K with the greedy pick: fused (kq_gemv_q8k_argmax) against the GEMV
     followed by kq_argmax; two resident copies (1 GB) alternate so the cache does not serve them.
@@ -472,21 +514,31 @@ def head_extra(torch, rn, dev):
     lib = rn.lib
     p = lambda t: C.c_void_p(t.data_ptr())
 
+    # each graph holds ROUNDS rounds of the two copies: replaying a graph costs several us between
+    # replays, which a graph of two launches would charge to the kernel
+    ROUNDS = 8
+
     def fused():
-        for w in ws_w:
+        for w in ws_w * ROUNDS:
             rn.check(lib.kq_gemv_q8k_argmax(p(w), R, C_, 14, p(xq), p(y), p(aws), p(out), rn.stream()))
 
     def separate():
-        for w in ws_w:
+        for w in ws_w * ROUNDS:
             rn.gemv(w, R, C_, 14, xq, 1, y, rn.stream())
             rn.check(lib.kq_argmax(p(y), R, p(aws), p(out), rn.stream()))
 
+    def gemv_only():
+        for w in ws_w * ROUNDS:
+            rn.gemv(w, R, C_, 14, xq, 1, y, rn.stream())
+
     res = {}
-    for name, fn in (("fused_us", fused), ("gemv_then_argmax_us", separate)):
+    for name, fn in (("gemv_us", gemv_only), ("fused_us", fused), ("gemv_then_argmax_us", separate)):
         g = capture(torch, fn)
-        time_graphs(torch, [g] * 3)
-        res[name] = round(time_graphs(torch, [g] * 10) / 20 * 1e6, 2)
+        res[name] = round(warm_then_time(torch, g, 2 * ROUNDS) * 1e6, 2)
     res["weight_GB/s_fused"] = round(wbytes(R, C_, 14) / (res["fused_us"] * 1e-6) / 1e9, 1)
+    nb6 = wbytes(R, C_, 14) + (C_ // 256) * Q8K + R * 4
+    res["gemv_GB/s"] = round(nb6 / (res["gemv_us"] * 1e-6) / 1e9, 1)
+    res["gemv_hbm_frac"] = round(nb6 / (res["gemv_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     del ws_w, w0
     # the real model's output size as Q4_K (output.weight 248320x4096, q4pack.py:22): random block
     # bytes with fp16 scales of a N(0, 0.02) row; the Q4_K GEMV's rate where the launch cost is
@@ -502,17 +554,16 @@ def head_extra(torch, rn, dev):
     y4 = torch.empty(R4, device=dev)
 
     def gemv4():
-        for w in ws4:
+        for w in ws4 * ROUNDS:
             rn.gemv(w, R4, C_, 12, xq, 1, y4, rn.stream())
 
     def fused4():
-        for w in ws4:
+        for w in ws4 * ROUNDS:
             rn.check(lib.kq_gemv_q8k_argmax(p(w), R4, C_, 12, p(xq), p(y4), p(aws), p(out), rn.stream()))
 
     for name, fn in (("q4k_248320_gemv_us", gemv4), ("q4k_248320_fused_us", fused4)):
         g = capture(torch, fn)
-        time_graphs(torch, [g] * 3)
-        res[name] = round(time_graphs(torch, [g] * 10) / 20 * 1e6, 2)
+        res[name] = round(warm_then_time(torch, g, 2 * ROUNDS) * 1e6, 2)
     nb = wbytes(R4, C_, 12) + (C_ // 256) * Q8K + R4 * 4
     res["q4k_248320_GB/s"] = round(nb / (res["q4k_248320_gemv_us"] * 1e-6) / 1e9, 1)
     res["q4k_248320_hbm_frac"] = round(nb / (res["q4k_248320_gemv_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
@@ -538,14 +589,15 @@ def gemm_extra(torch, rn, dev, timed=True):
                     rn.gemm(w, R, C_, ty, xq, M, y, ws, rn.stream())
                 torch.cuda.synchronize()
                 continue
-            g = capture(torch, lambda: rn.gemm(w, R, C_, ty, xq, M, y, ws, rn.stream()))
+            # 4 calls per graph: replaying a graph costs several us between replays
+            g = capture(torch, lambda: [rn.gemm(w, R, C_, ty, xq, M, y, ws, rn.stream()) for _ in range(4)])
             # warm-up of at least 0.2 s: the clock settles only after some ms of sustained MFMA
             # load (the first 10 calls run ~20 % slower than the steady state)
             warm = 0.0
             while warm < 0.2:
                 warm += time_graphs(torch, [g] * 20)
-            reps = 20
-            el = time_graphs(torch, [g] * reps) / reps
+            reps = 10
+            el = time_graphs(torch, [g] * reps) / (4 * reps)
             out["%s_M%d" % (name, M)] = {"us": round(el * 1e6, 1), "TOPS": round(2 * M * R * C_ / el / 1e12, 2),
                                          "frac_int8_peak": round(2 * M * R * C_ / el / 1e12 / INT8_PEAK_TOPS, 4)}
     return out
@@ -603,10 +655,11 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
-    ap.add_argument("--pmc-workload", choices=("gemv", "gemm"),
+    ap.add_argument("--pmc-workload", choices=("gemv", "gemm", "q6k"),
                     help="no timing, for rocprofv3 --pmc runs: 'gemv' launches the roofline kernel's "
                          "workload once per layer copy, then one 64 MiB device copy (the calibration "
-                         "kernel); 'gemm' runs each prefill GEMM shape twice")
+                         "kernel); 'gemm' runs each prefill GEMM shape twice; 'q6k' runs the Q6_K head and down "
+                         "projection GEMVs (and the Q4_K head) a few times")
     a = ap.parse_args()
     if a.steps < 1 or a.warmup < 0 or a.copies < 1:
         ap.error("--steps and --copies must be positive, --warmup not negative")
@@ -621,6 +674,9 @@ def main():
     rn = Runner(torch)
     if a.pmc_workload == "gemm":
         gemm_extra(torch, rn, dev, timed=False)
+        return
+    if a.pmc_workload == "q6k":
+        pmc_workload_q6k(torch, rn, dev)
         return
     log("bench: building %d resident layer copies" % a.copies)
     layers = make_layer(torch, dev, a.copies)

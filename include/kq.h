@@ -121,7 +121,8 @@ int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const in
  * equal largest values; NaN is never chosen and an input with no value above -1e30 gives 0.  The
  * rule of k_argmax (scripts/kindi_q4/kindi/kindi.cu:637-661), launched after the head GEMV by
  * Engine.head (engine.py:323-331).  One launch: workgroups reduce their share and the last one to
- * finish reduces the partials.  ws: kq_argmax_workspace() bytes, 256-byte aligned, zero-filled
+ * finish reduces the partials.  ws: kq_argmax_workspace() bytes (8320: 64 keys and a counter, each
+ * on its own cache line, so that atomics on one address stay few), 256-byte aligned, zero-filled
  * before its first use (each call leaves it ready for the next); calls sharing a workspace must be
  * ordered (same stream or synchronised).  out: one device int.
  */

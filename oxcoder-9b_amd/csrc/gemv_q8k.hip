@@ -3,7 +3,8 @@
 // Work unit: RPW consecutive rows of one 8-row tile of one matrix.  Up to three matrices that
 // share the activation (q/k/v, gate/up) are one launch: their units are numbered back to back.
 // The grid is sized to the chip (KQ_GEMV_WAVES_PER_CU waves per CU, fewer if there are fewer
-// units) and each wave walks units u = wave, wave + nwaves, ...; while it computes one
+// units) and each wave walks its units in increasing order, the waves of one workgroup sharing
+// whole 8-row tiles (TileWalk); while it computes one
 // (unit, column pass) it already has the loads of the next one in flight, so weight streaming
 // and the dot/reduce work of a wave overlap instead of alternating.
 //
@@ -54,6 +55,9 @@
 #ifndef KQ_XCDS
 #define KQ_XCDS 8          // accelerator complex dies per MI355X; workgroups alternate between them
 #endif
+#ifndef KQ_GEMV_TILE_WG
+#define KQ_GEMV_TILE_WG 1  // every 8-row tile is walked by the waves of one workgroup (see TileWalk)
+#endif
 
 namespace kq {
 
@@ -63,6 +67,40 @@ struct MatGroup {
     int64_t ldy[3];
     int first_unit[4];   // units of matrix m are [first_unit[m], first_unit[m+1])
     int n;
+};
+
+// Unit order of a wave (stream s of S streams in workgroup b of nwg; units of one 8-row tile:
+// WPT).  With S >= WPT the streams of a workgroup hold whole tiles when numbered consecutively:
+// unit = b*S + s + k*nwg*S.  With S < WPT (one-row Q6_K units over 4 streams, or several column
+// passes per stream) the workgroup takes tiles b, b + nwg, ... and stream s walks units s, s + S,
+// ... of each, so a tile's rows, whose 144- or 210-byte blocks share 128-byte lines with their
+// neighbours', are read through the L2 of one XCD instead of two (the 4096x12288 Q6_K down and the
+// 151936x4096 Q6_K head fetched 12 % more than their bytes from HBM with the tiles split).  TM =
+// false keeps the consecutive numbering: the sequential kernel's Q6_K down projection measured
+// 11.7 us with it and 12.2 us tile-major; the pass-split kernel gained from it (Q4_K two tokens
+// 12288x4096 10.0 -> 9.5 us, the fused 248320x4096 head 113 -> 105 us; the Q6_K head unchanged).
+template <int WPT, bool TM = true> struct TileWalk {
+    int b, nwg, s, S;
+    __device__ __forceinline__ bool tile_major() const { return TM && KQ_GEMV_TILE_WG && S < WPT; }
+    __device__ __forceinline__ int first() const { return tile_major() ? b * WPT + s : b * S + s; }
+    __device__ __forceinline__ int next(int u) const {
+        if (!tile_major()) return u + nwg * S;
+        return (u % WPT) + S < WPT ? u + S : u + nwg * WPT + S - WPT;
+    }
+    // the k-th unit of the stream, and how many units it walks in all
+    __device__ __forceinline__ int unit(int k) const {
+        if (!tile_major()) return b * S + s + k * nwg * S;
+        const int per = WPT / S;
+        return (b + (k / per) * nwg) * WPT + s + (k % per) * S;
+    }
+    __device__ __forceinline__ int count(int total_units) const {
+        if (!tile_major()) {
+            const int u0 = b * S + s;
+            return u0 < total_units ? (total_units - u0 + nwg * S - 1) / (nwg * S) : 0;
+        }
+        const int tiles = total_units / WPT;
+        return b < tiles ? ((tiles - b - 1) / nwg + 1) * (WPT / S) : 0;
+    }
 };
 
 // ------------------------------------------------------------------ per-type fragments
@@ -190,9 +228,10 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     const int lane = threadIdx.x & 63;
-    const int nwaves = gridDim.x * (blockDim.x >> 6);
     // Unit bookkeeping is wave-uniform: readfirstlane keeps it in scalar registers.
-    int u = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const TileWalk<WPT, false> walk{(int)blockIdx.x, (int)gridDim.x, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+                                    (int)(blockDim.x >> 6)};
+    int u = walk.first();
     if (u >= total_units) return;
     const int p = lane & 3, slot = lane >> 2;
     const int passes = ONEPASS ? 1 : FP ? FP : (G + 15) >> 4;
@@ -248,7 +287,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
     // number of loads in flight stays fixed.
     auto step = [&](Frag<TYPE>* cur, Frag<TYPE>* nxt) -> bool {
         int un = u, pn = pass + 1;
-        if (pn == passes) { pn = 0; un = u + nwaves; }
+        if (pn == passes) { pn = 0; un = walk.next(u); }
         const bool has_next = un < total_units;
         int mn = m;
         int64_t row0n = row0;
@@ -298,7 +337,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
         auto stepf = [&](auto pass_c, Frag<TYPE>* cur, Frag<TYPE>* nxt) -> bool {
             constexpr int PS = decltype(pass_c)::value;
             constexpr int PN = PS + 1 == FP ? 0 : PS + 1;
-            const int un = PN == 0 ? u + nwaves : u;
+            const int un = PN == 0 ? walk.next(u) : u;
             const bool has_next = un < total_units;
             int mn = m;
             int64_t row0n = row0;
@@ -350,7 +389,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
 // ------------------------------------------------------------------ pass-split kernel
 // For C <= 16384 (at most 4 column passes).  A workgroup holds K unit streams of P waves each
 // (P = passes): wave (stream, pass) keeps the activations of its pass in registers and streams
-// that pass's tile columns for every unit of its stream (units s, s + nstreams, ...),
+// that pass's tile columns for every unit of its stream (TileWalk order),
 // prefetching the next unit.  Each (unit, token, row) pass value goes to LDS; after one barrier
 // the workgroup merges them with the same pass tree as the sequential kernel and stores y.  With
 // one pass the value is stored directly.
@@ -367,15 +406,14 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pass = wave % P, stream = wave / P;
-    // Stream sid takes units sid, sid + nstreams, ...  With one pass (K = 4 streams per
-    // workgroup) the WPT units of an 8-row tile fall to the waves of one workgroup, so the rows
+    // The WPT units of an 8-row tile fall to the streams of one workgroup (TileWalk), so the rows
     // that share cache lines (144- and 210-byte blocks do not align to 128-byte lines) are read by
     // one CU through one L2.  (Contiguous unit ranges per stream, with the streams of each XCD
     // grouped, were slower: gate+up 12.2 -> 13.1 us, the output head 95 -> 108 us.)
     const int nwg = gridDim.x;
     const int lwg = blockIdx.x;
-    const int sid = lwg * K + stream, nstreams = nwg * K;
-    const int u_begin = sid, u_step = nstreams, u_end = total_units;
+    const TileWalk<WPT> walk{lwg, nwg, stream, K};
+    const int u_begin = walk.first(), u_end = total_units;
     const int p = lane & 3, slot = lane >> 2;
     const int64_t col_bytes = 8 * BS;
     const int64_t tile_bytes = (int64_t)G * col_bytes;
@@ -392,7 +430,7 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
         return mg.w[m] + tile * tile_bytes + r0 * BS + gc * col_bytes;
     };
 
-    ArgBest best = arg_init();                         // AMAX: this lane's best output (lane 0)
+    ArgBest best = arg_init();                         // AMAX: the wave's best output so far (every lane)
     if (u_begin < u_end) {
         Act<TYPE> act[NT];
 #pragma unroll
@@ -407,7 +445,7 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
         float* mypart = part + (int64_t)stream * kmax * NT * RPW * P;
 
         auto step = [&](Frag<TYPE>* cur, Frag<TYPE>* nxt) -> bool {
-            const int un = u + u_step;
+            const int un = walk.next(u);
             const bool has_next = un < u_end;
             int mn = m;
             int64_t row0n = row0;
@@ -424,11 +462,11 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
                     const float v = block_value(fr, act[t], p);
                     const float pv = slot_tree_f32(valid ? v : 0.0f);
                     if (P == 1) {
-                        if (lane == 0) {
-                            const float yv = __fadd_rn(pv, 0.0f);
-                            mg.y[m][t * mg.ldy[m] + row0 + r] = yv;
-                            if (AMAX) arg_take(best, yv, (int)(row0 + r));
-                        }
+                        // every lane holds the same pv (the slot tree is symmetric); the units of a
+                        // stream come in increasing row order, so the pick runs unmasked
+                        const float yv = __fadd_rn(pv, 0.0f);
+                        if (lane == 0) mg.y[m][t * mg.ldy[m] + row0 + r] = yv;
+                        if (AMAX) arg_take_ascending(best, yv, (int)(row0 + r));
                     } else if (lane == 0) {
                         mypart[((k * NT + t) * RPW + r) * P + pass] = pv;
                     }
@@ -448,13 +486,12 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
 
     __syncthreads();
     for (int st = 0; st < K; st++) {
-        const int s0 = lwg * K + st;
-        const int b0 = s0, bstep = nstreams;
-        const int nk = b0 < total_units ? (total_units - b0 + nstreams - 1) / nstreams : 0;
+        const TileWalk<WPT> ws{lwg, nwg, st, K};
+        const int nk = ws.count(total_units);
         const float* sp = part + (int64_t)st * kmax * NT * RPW * P;
         for (int idx = threadIdx.x; idx < nk * NT * RPW; idx += blockDim.x) {
             const int kk = idx / (NT * RPW), t = (idx / RPW) % NT, r = idx % RPW;
-            const int uu = b0 + kk * bstep;
+            const int uu = ws.unit(kk);
             const int mm = uu >= mg.first_unit[1] ? (uu >= mg.first_unit[2] ? 2 : 1) : 0;
             const int v = uu - mg.first_unit[mm];
             const int64_t rowr = (int64_t)(v / WPT) * 8 + (v % WPT) * RPW + r;
@@ -511,8 +548,11 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
         size_t lds = 0;
         int kmax = 1;
         if (passes > 1) {
+            constexpr int WPT = 8 / RPW;
             for (;;) {
-                kmax = (total + nwg * K - 1) / (nwg * K);
+                // most units a stream walks (TileWalk::count)
+                kmax = KQ_GEMV_TILE_WG && K < WPT ? (total / WPT + nwg - 1) / nwg * (WPT / K)
+                                                  : (total + nwg * K - 1) / (nwg * K);
                 lds = (size_t)K * kmax * NT * RPW * passes * sizeof(float);
                 if (lds <= 32768 || nwg * K >= total) break;
                 nwg = round_xcd(nwg * 2);

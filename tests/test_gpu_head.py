@@ -43,6 +43,8 @@ def test_argmax_vs_oracle_and_repeated_calls(dev, orc):
         for name, y in argmax_cases():
             ops.argmax(dev_t(y, dev), ws, out)
             assert pick(out) == orc.argmax(y), (name, rep)
+    torch.cuda.synchronize()
+    assert int(ws.to(torch.int32).abs().sum()) == 0           # every call leaves it zero for the next
 
 
 def head_matrix(R, C, ty, seed, dup=None):

@@ -404,28 +404,48 @@ def producers_extra(torch, rn, layers, dev, steps=320):
 
 
 def f32_layer_extra(torch, rn, layers, dev, steps=320):
-    """The fp32-activation drop-in for q4_gemv (kq_gemv: Kindi's numerics, no activation
-    quantization) over one decode layer's 7 matrices, one launch per matrix as gpu4.Engine.gemv
-    launches q4_gemv (gpu4.py:95-99); the resident layer copies rotate, replayed from a graph.
-    Algorithmic bytes: weights + fp32 input (C*4) + fp32 output (R*4) per matrix."""
+    """The fp32-activation drop-in for q4_gemv (Kindi's numerics, no activation quantization) over
+    one decode layer's 7 matrices, as Engine(mode="f32").gemv runs them: the matrices that share an
+    input in one kq_gemv_multi launch (q/k/v, gate/up), o and down alone (4 launches; the
+    reference launches q4_gemv once per matrix, gpu4.py:95-99); also one kq_gemv launch per matrix
+    (7 launches).  The resident layer copies rotate, replayed from graphs.  Algorithmic bytes:
+    weights + fp32 input (C*4) once per launch + fp32 output (R*4) per matrix."""
     from kq import quantize as kqq
     xs = [torch.from_numpy(kqq.synthetic_activations(1, c, seed=s)[0]).to(dev) for s, c in enumerate(INPUT_COLS)]
     ys = {name: torch.empty(R, device=dev) for name, R, _, _, _ in LAYER}
     p = lambda t: C.c_void_p(t.data_ptr())
 
-    def run_all():
+    def grouped():
+        s = rn.stream()
+        for lay in layers:
+            for slot, C_ in enumerate(INPUT_COLS):
+                g = [(n, R, ty) for n, R, C2, ty, sl in LAYER if sl == slot]
+                k = len(g)
+                W = (C.c_void_p * k)(*[lay[n].data_ptr() for n, _, _ in g])
+                Rs = (C.c_int * k)(*[R for _, R, _ in g])
+                Ts = (C.c_int * k)(*[ty for _, _, ty in g])
+                Y = (C.c_void_p * k)(*[ys[n].data_ptr() for n, _, _ in g])
+                rn.check(rn.lib.kq_gemv_multi(k, W, Rs, C_, Ts, p(xs[slot]), Y, s))
+
+    def per_matrix():
         s = rn.stream()
         for lay in layers:
             for name, R, C_, ty, slot in LAYER:
                 rn.check(rn.lib.kq_gemv(p(lay[name]), R, C_, ty, p(xs[slot]), p(ys[name]), s))
 
-    g = capture(torch, run_all)
-    time_graphs(torch, [g] * 2)
+    out = {}
     reps = max(1, steps // len(layers))
-    per = time_graphs(torch, [g] * reps) / (reps * len(layers))
-    nbytes = sum(wbytes(R, C_, ty) + C_ * 4 + R * 4 for _, R, C_, ty, _ in LAYER)
-    return {"layer_us": round(per * 1e6, 2), "bytes_per_layer": nbytes,
-            "GB/s": round(nbytes / per / 1e9, 1), "hbm_frac": round(nbytes / per / 1e9 / HBM_PEAK_GBS, 4)}
+    for tag, fn in (("", grouped), ("per_matrix_", per_matrix)):
+        g = capture(torch, fn)
+        time_graphs(torch, [g] * 2)
+        per = time_graphs(torch, [g] * reps) / (reps * len(layers))
+        launches = len(INPUT_COLS) if not tag else len(LAYER)
+        nbytes = sum(wbytes(R, C_, ty) + R * 4 for _, R, C_, ty, _ in LAYER)
+        nbytes += (sum(INPUT_COLS) if not tag else sum(C_ for _, _, C_, _, _ in LAYER)) * 4
+        out.update({tag + "layer_us": round(per * 1e6, 2), tag + "launches": launches, tag + "bytes_per_layer": nbytes,
+                    tag + "GB/s": round(nbytes / per / 1e9, 1),
+                    tag + "hbm_frac": round(nbytes / per / 1e9 / HBM_PEAK_GBS, 4)})
+    return out
 
 
 def pack_extra(torch, dev, layers=2):

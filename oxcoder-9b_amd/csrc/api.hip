@@ -80,7 +80,9 @@ int kq_gemv(const void* w, int R, int C, int type, const float* x, float* y, voi
     KQ_TRY(check_matrix(w, R, C, type, fn));
     KQ_TRY(check_ptr(x, 4, "x", fn));
     KQ_TRY(check_ptr(y, 4, "y", fn));
-    launch_gemv_f32(static_cast<const uint8_t*>(w), R, C, type, x, y, 0, as_stream(stream));
+    if (R / 8 > (1 << 27)) return fail(KQ_ERR_ARG, "%s: R=%d too large for one call", fn, R);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    launch_gemv_f32_group(1, &wb, &R, C, type, x, &y, as_stream(stream));
     return check_launch(fn);
 }
 
@@ -89,13 +91,24 @@ int kq_gemv_multi(int n, const void* const* w, const int* R, int C, const int* t
     static const char* fn = "kq_gemv_multi";
     if (n < 1 || n > 3) return fail(KQ_ERR_ARG, "%s: n=%d must be 1..3", fn, n);
     if (!w || !R || !type || !y) return fail(KQ_ERR_ARG, "%s: NULL array argument", fn);
+    int64_t tiles = 0;
     for (int i = 0; i < n; i++) {
         KQ_TRY(check_matrix(w[i], R[i], C, type[i], fn));
         KQ_TRY(check_ptr(y[i], 4, "y[i]", fn));
+        tiles += R[i] / 8;
     }
+    if (tiles > (1 << 27)) return fail(KQ_ERR_ARG, "%s: too many rows in one call", fn);
     KQ_TRY(check_ptr(x, 4, "x", fn));
-    for (int i = 0; i < n; i++)
-        launch_gemv_f32(static_cast<const uint8_t*>(w[i]), R[i], C, type[i], x, y[i], 0, as_stream(stream));
+    // matrices of the same type share a launch
+    for (int ty : {KQ_TYPE_Q4_K, KQ_TYPE_Q6_K}) {
+        const uint8_t* ws[3];
+        int rs[3];
+        float* ys[3];
+        int k = 0;
+        for (int i = 0; i < n; i++)
+            if (type[i] == ty) { ws[k] = static_cast<const uint8_t*>(w[i]); rs[k] = R[i]; ys[k] = y[i]; k++; }
+        if (k) launch_gemv_f32_group(k, ws, rs, C, ty, x, ys, as_stream(stream));
+    }
     return check_launch(fn);
 }
 

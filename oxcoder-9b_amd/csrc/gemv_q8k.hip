@@ -218,13 +218,129 @@ __device__ __forceinline__ float block_value(const Q6Fields& f, const Act<TYPE_Q
     return q6k_value(f16_lo(f.dw >> (8 * f.sh)), a.dx, I);
 }
 
+// ------------------------------------------------------------------ fp32 activations
+// The same lanes and weight fragments with fp32 activations (Kindi's q4_gemv numerics,
+// q4.cu:18-27): a lane keeps its 64 activations of the column and their sums, and per weight
+// converts the code to fp32 (v_cvt_f32_ubyte) and accumulates with fp32 FMA; per sub-block the
+// decoded scale is applied to the sum, w = (d*sc)*q - dmin*m, as
+//   sum_j w_j x_j = (d*sc_lo) * sum_j q_j x_j - (dmin*m_lo) * sum_j x_j   (Q4_K, likewise hi)
+//                 = (d*sc_k) * (sum_j q6u_j x_j - 32 * sum_j x_j)           (Q6_K, q6u = q + 32).
+// The quad's four partial values are added in fp32 (lanes p^1, then p^2: the same bits in the four
+// lanes) and go through the slot and pass trees like the Q8_K values.
+template <int TYPE> struct ActF;
+template <> struct ActF<TYPE_Q4_K> { float xl[32], xh[32], sxl, sxh; };   // elements 64p + 0..31, 64p + 32..63
+template <> struct ActF<TYPE_Q6_K> { float xa[64], sx[4]; };             // xa[16k + j]: element 128h + 32k + 16jj + j
+
+__device__ __forceinline__ float ubf(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xffu); }
+// acc + sum over the 4 bytes of q (codes) times x[0..3], in byte order
+__device__ __forceinline__ float dot_bytes_f32(uint32_t q, const float* x, float acc) {
+    acc = __builtin_fmaf(ubf(q, 0), x[0], acc);
+    acc = __builtin_fmaf(ubf(q, 1), x[1], acc);
+    acc = __builtin_fmaf(ubf(q, 2), x[2], acc);
+    return __builtin_fmaf(ubf(q, 3), x[3], acc);
+}
+
+// xg = the 256 activations of column g.
+__device__ __forceinline__ void load_act(ActF<TYPE_Q4_K>& a, const float* xg, int p) {
+    const float* x = xg + 64 * p;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const f32x4 lo = *reinterpret_cast<const f32x4_a4*>(x + 4 * k);
+        const f32x4 hi = *reinterpret_cast<const f32x4_a4*>(x + 32 + 4 * k);
+        a.xl[4 * k] = lo.x; a.xl[4 * k + 1] = lo.y; a.xl[4 * k + 2] = lo.z; a.xl[4 * k + 3] = lo.w;
+        a.xh[4 * k] = hi.x; a.xh[4 * k + 1] = hi.y; a.xh[4 * k + 2] = hi.z; a.xh[4 * k + 3] = hi.w;
+    }
+    a.sxl = 0.0f;
+    a.sxh = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) { a.sxl = __fadd_rn(a.sxl, a.xl[j]); a.sxh = __fadd_rn(a.sxh, a.xh[j]); }
+}
+__device__ __forceinline__ void load_act(ActF<TYPE_Q6_K>& a, const float* xg, int p) {
+    const int h = p >> 1, jj = p & 1;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float* x = xg + h * 128 + k * 32 + 16 * jj;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + 4 * w);
+            a.xa[16 * k + 4 * w] = v.x; a.xa[16 * k + 4 * w + 1] = v.y;
+            a.xa[16 * k + 4 * w + 2] = v.z; a.xa[16 * k + 4 * w + 3] = v.w;
+        }
+        float sx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) sx = __fadd_rn(sx, a.xa[16 * k + j]);
+        a.sx[k] = sx;
+    }
+}
+__device__ __forceinline__ float quad_sum_f32(float v) {
+    v = __fadd_rn(v, __shfl_xor(v, 1, 64));
+    return __fadd_rn(v, __shfl_xor(v, 2, 64));
+}
+__device__ __forceinline__ float block_value(const Frag<TYPE_Q4_K>& f, const ActF<TYPE_Q4_K>& a, int p) {
+    const ScMin sm = q4k_scmin_pair(f.hdr.y, f.hdr.z, f.hdr.w, p);
+    const uint32_t q[8] = {f.qa.x, f.qa.y, f.qa.z, f.qa.w, f.qb.x, f.qb.y, f.qb.z, f.qb.w};
+    float plo = 0.0f, phi = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        plo = dot_bytes_f32(q[k] & 0x0f0f0f0fu, a.xl + 4 * k, plo);
+        phi = dot_bytes_f32((q[k] >> 4) & 0x0f0f0f0fu, a.xh + 4 * k, phi);
+    }
+    const float d = f16_lo(f.hdr.x), dm = f16_hi(f.hdr.x);
+    const float dsl = __fmul_rn(d, (float)sm.sc_lo), dsh = __fmul_rn(d, (float)sm.sc_hi);
+    const float msl = __fmul_rn(dm, (float)sm.m_lo), msh = __fmul_rn(dm, (float)sm.m_hi);
+    const float lo = __fsub_rn(__fmul_rn(dsl, plo), __fmul_rn(msl, a.sxl));
+    const float hi = __fsub_rn(__fmul_rn(dsh, phi), __fmul_rn(msh, a.sxh));
+    return quad_sum_f32(__fadd_rn(lo, hi));
+}
+__device__ __forceinline__ float block_value(const Q6Fields& f, const ActF<TYPE_Q6_K>& a, int p) {
+    const int jj = p & 1;
+    const uint32_t w0 = __builtin_amdgcn_alignbyte(f.sc.y, f.sc.x, f.sh);   // scales 8h .. 8h+3
+    const uint32_t w1 = __builtin_amdgcn_alignbyte(f.sce, f.sc.y, f.sh);    // scales 8h+4 .. 8h+7
+    const u32x4 l0 = funnel(f.l0, f.l0e, f.sh), l1 = funnel(f.l1, f.l1e, f.sh), hb = funnel(f.hb, f.hbe, f.sh);
+    const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
+    const uint32_t H[4] = {hb.x, hb.y, hb.z, hb.w};
+    float P[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t m4 = 0x0f0f0f0fu, m2 = 0x30303030u;
+        P[0] = dot_bytes_f32((L0[w] & m4) | ((H[w] << 4) & m2), a.xa + 0 * 16 + 4 * w, P[0]);
+        P[1] = dot_bytes_f32((L1[w] & m4) | ((H[w] << 2) & m2), a.xa + 1 * 16 + 4 * w, P[1]);
+        P[2] = dot_bytes_f32(((L0[w] >> 4) & m4) | (H[w] & m2), a.xa + 2 * 16 + 4 * w, P[2]);
+        P[3] = dot_bytes_f32(((L1[w] >> 4) & m4) | ((H[w] >> 2) & m2), a.xa + 3 * 16 + 4 * w, P[3]);
+    }
+    const float d = f16_lo(f.dw >> (8 * f.sh));
+    const int sc[4] = {sbyte(w0, jj), sbyte(w0, jj + 2), sbyte(w1, jj), sbyte(w1, jj + 2)};
+    float v = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        v = __fadd_rn(v, __fmul_rn(__fmul_rn(d, (float)sc[k]), __fsub_rn(P[k], __fmul_rn(32.0f, a.sx[k]))));
+    return quad_sum_f32(v);
+}
+
+// Activation formats of the kernels below: where column g of token t starts, and its register type.
+struct ActQ8K {
+    template <int T> using A = Act<T>;
+    static constexpr bool F32 = false;
+    static __device__ __forceinline__ const uint8_t* col(const uint8_t* X, int64_t t, int G, int g) {
+        return X + (t * G + g) * Q8K_BYTES;
+    }
+};
+struct ActF32 {
+    template <int T> using A = ActF<T>;
+    static constexpr bool F32 = true;
+    static __device__ __forceinline__ const float* col(const uint8_t* X, int64_t t, int G, int g) {
+        return reinterpret_cast<const float*>(X) + (t * G + g) * QK;
+    }
+};
+
 // ------------------------------------------------------------------ the kernel
 // FP = 3: exactly three column passes (C = 8448 .. 12288, the FFN down projection), with the
 // activations of all three held in registers instead of reloaded at every (unit, pass) step;
 // the step loop is unrolled over the passes so each step's pass is a compile-time index.
-template <int TYPE, int NT, int RPW, bool ONEPASS, int FP = 0>
+template <int TYPE, int NT, int RPW, bool ONEPASS, int FP = 0, class AP = ActQ8K>
 __global__ void __launch_bounds__(256)
 k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) {
+    using ActT = typename AP::template A<TYPE>;
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     const int lane = threadIdx.x & 63;
@@ -253,18 +369,18 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
     // values are masked to zero), so the number of loads in flight is static and the compiler
     // can wait for the current step's data without draining the next step's prefetch.
     const int slot_c = slot < G ? slot : G - 1;
-    Act<TYPE> act[NT];
+    ActT act[NT];
     if (ONEPASS) {
 #pragma unroll
-        for (int t = 0; t < NT; t++) load_act(act[t], XQ + ((int64_t)t * G + slot_c) * Q8K_BYTES, p);
+        for (int t = 0; t < NT; t++) load_act(act[t], AP::col(XQ, t, G, slot_c), p);
     }
-    Act<TYPE> actp[FP ? FP : 1][NT];                   // FP: every pass's activations
+    ActT actp[FP ? FP : 1][NT];                        // FP: every pass's activations
     if (FP) {
 #pragma unroll
         for (int q = 0; q < (FP ? FP : 1); q++) {
             const int gq = slot + 16 * q < G ? slot + 16 * q : G - 1;
 #pragma unroll
-            for (int t = 0; t < NT; t++) load_act(actp[q][t], XQ + ((int64_t)t * G + gq) * Q8K_BYTES, p);
+            for (int t = 0; t < NT; t++) load_act(actp[q][t], AP::col(XQ, t, G, gq), p);
         }
     }
 
@@ -306,7 +422,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
         if (!ONEPASS) {
             const int gc = valid ? g : G - 1;
 #pragma unroll
-            for (int t = 0; t < NT; t++) load_act(act[t], XQ + ((int64_t)t * G + gc) * Q8K_BYTES, p);
+            for (int t = 0; t < NT; t++) load_act(act[t], AP::col(XQ, t, G, gc), p);
         }
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
@@ -395,10 +511,11 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
 // one pass the value is stored directly.
 // AMAX (one matrix, one token, one pass): the argmax of the outputs as well, into *aout
 // (argmax_block.h; aws is its workspace).
-template <int TYPE, int NT, int RPW, bool AMAX>
+template <int TYPE, int NT, int RPW, bool AMAX, class AP = ActQ8K>
 __global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
 k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units, int P, int kmax,
                  uint8_t* aws, int* aout) {
+    using ActT = typename AP::template A<TYPE>;
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     extern __shared__ float part[];                    // [stream][k][t][r][pass]
@@ -432,9 +549,9 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
 
     ArgBest best = arg_init();                         // AMAX: the wave's best output so far (every lane)
     if (u_begin < u_end) {
-        Act<TYPE> act[NT];
+        ActT act[NT];
 #pragma unroll
-        for (int t = 0; t < NT; t++) load_act(act[t], XQ + ((int64_t)t * G + gc) * Q8K_BYTES, p);
+        for (int t = 0; t < NT; t++) load_act(act[t], AP::col(XQ, t, G, gc), p);
 
         Frag<TYPE> bufA[RPW], bufB[RPW];
         int u = u_begin, k = 0, m;
@@ -523,7 +640,7 @@ static int pick_rpw(int nt, int type, int G) {
 #endif
 }
 
-template <int TYPE, int NT, int RPW, bool AMAX = false>
+template <int TYPE, int NT, int RPW, bool AMAX = false, class AP = ActQ8K>
 static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s, uint8_t* aws = nullptr,
                     int* aout = nullptr) {
     MatGroup mg = mg0;
@@ -537,7 +654,8 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
     const int wpc = TYPE == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_Q6 : KQ_GEMV_WAVES_PER_CU;
     // Q6_K with one or two tokens: sequential passes (the activations are reloaded per pass,
     // which only pays off while they are few)
-    if (passes <= (TYPE == TYPE_Q6_K && NT <= 2 ? KQ_GEMV_SPLIT_MAX_Q6 : KQ_GEMV_SPLIT_MAX)) {
+    // (fp32 activations keep 64 floats per lane and pass: every pass a wave of its own)
+    if (passes <= (TYPE == TYPE_Q6_K && NT <= 2 && !AP::F32 ? KQ_GEMV_SPLIT_MAX_Q6 : KQ_GEMV_SPLIT_MAX)) {
         // K unit streams of `passes` waves per workgroup (about KQ_GEMV_WG_WAVES waves per
         // workgroup); about KQ_GEMV_WAVES_PER_CU waves per CU in total
         const int K = passes >= KQ_GEMV_WG_WAVES ? 1 : KQ_GEMV_WG_WAVES / passes;
@@ -558,24 +676,24 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
                 nwg = round_xcd(nwg * 2);
             }
         }
-        hipLaunchKernelGGL((k_gemv_q8k_split<TYPE, NT, RPW, AMAX>), dim3(nwg), dim3(64 * passes * K), lds, s, mg, xq,
-                           G, total, passes, kmax, aws, aout);
+        hipLaunchKernelGGL((k_gemv_q8k_split<TYPE, NT, RPW, AMAX, AP>), dim3(nwg), dim3(64 * passes * K), lds, s, mg,
+                           xq, G, total, passes, kmax, aws, aout);
         return;
     }
     const int wpb = KQ_GEMV_SEQ_WPB;
     int waves = device_cus() * (TYPE == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_SEQ_Q6 : wpc);
     if (waves > total) waves = total;
     dim3 grid((waves + wpb - 1) / wpb), block(64 * wpb);
-    if constexpr (KQ_GEMV_P3 && NT <= 2 && RPW <= 2) {
+    if constexpr (KQ_GEMV_P3 && NT <= 2 && RPW <= 2 && !AP::F32) {
         if (passes == 3) {
             hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false, 3>), grid, block, 0, s, mg, xq, G, total);
             return;
         }
     }
     if (G <= 16)
-        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, true>), grid, block, 0, s, mg, xq, G, total);
+        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, true, 0, AP>), grid, block, 0, s, mg, xq, G, total);
     else
-        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false>), grid, block, 0, s, mg, xq, G, total);
+        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false, 0, AP>), grid, block, 0, s, mg, xq, G, total);
 }
 
 template <int TYPE, int NT>
@@ -648,6 +766,27 @@ void launch_gemv_q8k_argmax(const uint8_t* w, int R, int C, int type, const uint
 void launch_gemv_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N, float* y,
                      int64_t ldy, hipStream_t s) {
     launch_gemv_q8k_group(1, &w, &R, C, type, xq, N, &y, &ldy, s);
+}
+
+// fp32 activations: n (1..3) matrices of one type sharing x, one launch.  Two rows per unit for
+// Q4_K, one for Q6_K, as the Q8_K GEMV takes them.
+void launch_gemv_f32_group(int n, const uint8_t* const* w, const int* R, int C, int type, const float* x,
+                           float* const* y, hipStream_t s) {
+    const int G = C / QK;
+    MatGroup mg{};
+    mg.n = n;
+    int tiles = 0;
+    for (int i = 0; i < n; i++) {
+        mg.w[i] = w[i];
+        mg.y[i] = y[i];
+        mg.ldy[i] = R[i];
+        mg.first_unit[i] = tiles;
+        tiles += R[i] / 8;
+    }
+    for (int i = n; i < 4; i++) mg.first_unit[i] = tiles;
+    const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
+    if (type == TYPE_Q4_K) launch3<TYPE_Q4_K, 1, 2, false, ActF32>(mg, xb, G, s);
+    else launch3<TYPE_Q6_K, 1, 1, false, ActF32>(mg, xb, G, s);
 }
 
 }  // namespace kq

@@ -55,8 +55,10 @@ void launch_gemv_q8k_argmax(const uint8_t* w, int R, int C, int type, const uint
                             int* out, hipStream_t s);
 void launch_subblock_sums(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int N,
                           int32_t* sums, hipStream_t s);
-void launch_gemv_f32(const uint8_t* w, int R, int C, int type, const float* x, float* y,
-                     int rows_per_wave, hipStream_t s);
+// fp32-activation GEMV (Kindi numerics) of n (1..3) matrices of one type sharing x: the kernels of
+// the Q8_K GEMV with fp32 activations, one launch.
+void launch_gemv_f32_group(int n, const uint8_t* const* w, const int* R, int C, int type, const float* x,
+                           float* const* y, hipStream_t s);
 void launch_dequant_rows(const uint8_t* w, int R, int C, int type, int row0, int nrows, float* y,
                          int64_t ldy, hipStream_t s);
 

@@ -142,8 +142,9 @@ class Engine:
         for (w, R, _, _), y in zip(mats, outs):
             self._check_out(y, R)
         if self.mode == "f32":
-            for (w, R, C_, ty), y in zip(mats, outs):
-                ops.gemv(w, R, C_, ty, x, y)
+            # matrices sharing the input go three at a time into one launch per type (kcpu4.c:100-118)
+            for i in range(0, len(mats), 3):
+                ops.gemv_multi(mats[i:i + 3], x, outs[i:i + 3])
             return 1
         xq = self._quantize(x.reshape(1, -1)[:, :C], C)
         # matrices sharing the input go three at a time into one launch (kcpu4.c:100-118)

@@ -48,6 +48,26 @@ def gemv(w, R, C_, ty, x, y):
     return y
 
 
+def gemv_multi(mats, x, ys):
+    """Up to 3 matrices [(w, R, C, type)] sharing fp32 x [C], one launch per type (kq_gemv_multi;
+    the multi-matrix gemv of the CPU engine, kcpu4.c:100-118)."""
+    n = len(mats)
+    if not 1 <= n <= 3 or len(ys) != n:
+        raise ValueError("1..3 matrices with one output each")
+    C_ = mats[0][2]
+    if any(m[2] != C_ for m in mats) or x.numel() < C_:
+        raise ValueError("matrices sharing an input must have the same column count")
+    W = (C.c_void_p * n)(*[_weights(w, R, C_, ty).value for (w, R, _, ty) in mats])
+    Rs = (C.c_int * n)(*[m[1] for m in mats])
+    Ts = (C.c_int * n)(*[m[3] for m in mats])
+    for (w, R, _, ty), y in zip(mats, ys):
+        if y.numel() < R:
+            raise ValueError("output too small")
+    Y = (C.c_void_p * n)(*[_dev(y, "y", torch.float32).value for y in ys])
+    _lib.check(_lib.kq().kq_gemv_multi(n, W, Rs, C_, Ts, _dev(x, "x", torch.float32), Y, _stream(mats[0][0].device)))
+    return ys
+
+
 def q8k_quantize(x, out=None):
     """x [N][C] fp32 (row stride x.stride(0)) -> Q8_K bytes uint8 [N][C/256*292]."""
     if x.dim() == 1:

@@ -675,6 +675,9 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
+    ap.add_argument("--only", choices=("batched", "producers", "f32_layer", "gemm", "head", "decode_stream", "pack"),
+                    help="run only this extra (no headline step, no CPU baseline) and print its JSON; for "
+                         "profiling one workload")
     ap.add_argument("--pmc-workload", choices=("gemv", "gemm", "q6k"),
                     help="no timing, for rocprofv3 --pmc runs: 'gemv' launches the roofline kernel's "
                          "workload once per layer copy, then one 64 MiB device copy (the calibration "
@@ -697,6 +700,18 @@ def main():
         return
     if a.pmc_workload == "q6k":
         pmc_workload_q6k(torch, rn, dev)
+        return
+    if a.only:
+        need_layers = a.only in ("producers", "f32_layer")
+        lay = make_layer(torch, dev, a.copies) if need_layers else None
+        fn = {"batched": lambda: batched_extra(torch, rn, dev, 160),
+              "producers": lambda: producers_extra(torch, rn, lay, dev),
+              "f32_layer": lambda: f32_layer_extra(torch, rn, lay, dev),
+              "gemm": lambda: gemm_extra(torch, rn, dev),
+              "head": lambda: head_extra(torch, rn, dev),
+              "decode_stream": lambda: decode_stream_extra(torch, rn, dev),
+              "pack": lambda: pack_extra(torch, dev)}[a.only]
+        print(json.dumps({a.only: fn()}), flush=True)
         return
     log("bench: building %d resident layer copies" % a.copies)
     layers = make_layer(torch, dev, a.copies)

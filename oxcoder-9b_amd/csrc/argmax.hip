@@ -22,8 +22,12 @@ __global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ y, int
 
 size_t argmax_workspace_bytes() { return ARGMAX_WS_BYTES; }
 
+#ifndef KQ_ARGMAX_PER_THREAD
+#define KQ_ARGMAX_PER_THREAD 16
+#endif
 void launch_argmax(const float* y, int n, uint8_t* ws, int* out, hipStream_t s) {
-    int nwg = (n + 256 * 16 - 1) / (256 * 16);             // about 16 values per thread
+    constexpr int per = KQ_ARGMAX_PER_THREAD;               // values per thread, about
+    int nwg = (n + 256 * per - 1) / (256 * per);
     nwg = nwg < 1 ? 1 : (nwg > 2 * device_cus() ? 2 * device_cus() : nwg);
     hipLaunchKernelGGL(k_argmax, dim3(nwg), dim3(256), 0, s, y, n, ws, out);
 }

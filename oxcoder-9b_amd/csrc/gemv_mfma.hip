@@ -1,4 +1,4 @@
-// Small-batch GEMV (speculative verify, 3..16 tokens) on int8 MFMA for gfx950.
+// Small-batch GEMV (speculative verify, 2..16 tokens) on int8 MFMA for gfx950.
 //
 // A wave owns 16 weight rows x 4 consecutive super-blocks (a "chunk") for all tokens: per
 // super-block it forms the exact integers of the GEMV (Q4_K: I1 = sum sc_s*S_s and
@@ -16,9 +16,15 @@
 // min term is one v_mfma_f32_16x16x16_f16 with exact small-integer operands [B_s >> 6, B_s & 63]
 // and [-64 m_s, -m_s], which returns -I2 exactly.
 //
-// MFMA lanes: lane l serves token (A operand) and weight row (B operand) l & 15 and K chunk
-// q = l >> 4 (16 bytes); K step p covers super-block elements 64p .. 64p+63, the lane's 16 are
-// 64p + 16q + i.  Outputs: lane l holds tokens 4q + j (j = 0..3) of row l & 15.
+// MFMA lanes: lane l serves token (A operand) and weight row (B operand) l & 15 and K slots
+// 16q .. 16q+15 of each step, q = l >> 4.  Outputs: lane l holds tokens 4q + j (j = 0..3) of row
+// l & 15.  Which super-block elements a K slot carries is free (the products are exact integer
+// sums), so each type uses the assignment that loads its bytes best:
+//   Q4_K: lane q reads qs bytes 32q .. 32q+31 (sub-blocks 2q and 2q+1, the GEMV's lane layout),
+//         each quant byte once per row; step p takes bytes 32q + 8p .. +7, low nibbles (elements
+//         64q + 8p + i) in slots 0..7 and high nibbles (64q + 32 + 8p + i) in slots 8..15, and
+//         the activation bytes of those elements come from the lane's 64 contiguous ones.
+//   Q6_K: step p covers elements 64p + 16q + i (h = p >> 1 selects the 128-element half).
 #include "kq_device.h"
 #include "kq_internal.h"
 #include "q4_lanes.h"
@@ -51,22 +57,22 @@ __device__ __forceinline__ uint32_t mv_pk_f16(float a, float b) {   // exact sma
 
 // ------------------------------------------------------------------ per-super-block operands
 template <int TYPE> struct MvW;
-// Q4_K: header and, per K step p, the 16 qs bytes 32p + 16(q & 1) .. +15 (low nibbles for q < 2).
-template <> struct MvW<TYPE_Q4_K> { u32x4 hdr, qs[4]; };
+// Q4_K: header and the lane's 32 qs bytes 32q .. 32q+31.
+template <> struct MvW<TYPE_Q4_K> { u32x4 hdr, qa, qb; };
 // Q6_K: dword-aligned raw words: ql bytes 64h + 16q (h = 0, 1), qh bytes 32h + 16(q & 1), the 16
 // scales and d, each 16-byte field with the dword after it; sh = block start & 3.
 template <> struct MvW<TYPE_Q6_K> { u32x4 ql[2], qh[2], sc; uint32_t qle[2], qhe[2], sce, sh; };
 
 struct MvX {
-    u32x4 a[4];     // activation bytes 64p + 16q .. +15 of token l & 15
+    u32x4 a[4];     // activation bytes of token l & 15: Q4_K 64q + 16k .. +15, Q6_K 64k + 16q .. +15
     u32x4 bs;       // bsums 8(q & 1) .. 8(q & 1) + 7 of token l & 15 (Q4_K min term)
     float dx[4];    // d of tokens 4q + j
 };
 
 __device__ __forceinline__ void mv_load(MvW<TYPE_Q4_K>& w, const uint8_t* bk, int q) {
     w.hdr = ld16(bk);
-#pragma unroll
-    for (int p = 0; p < 4; p++) w.qs[p] = ld16(bk + 16 + 32 * p + 16 * (q & 1));
+    w.qa = ld16(bk + 16 + 32 * q);
+    w.qb = ld16(bk + 32 + 32 * q);
 }
 // The last word read (bytes 208..211 from the aligned base) passes the block end by 2 bytes only
 // for blocks starting at 0 (mod 4), which are never row 7 of a tile column.
@@ -84,9 +90,10 @@ __device__ __forceinline__ void mv_load(MvW<TYPE_Q6_K>& w, const uint8_t* bk, in
     w.sce = ld4(b4 + 208);
 }
 // xa: Q8_K block of token l & 15; xd[j]: Q8_K block of token 4q + j (tokens clamped by the caller).
+template <int TYPE>
 __device__ __forceinline__ void mv_load_x(MvX& x, const uint8_t* xa, const uint8_t* const* xd, int q) {
 #pragma unroll
-    for (int p = 0; p < 4; p++) x.a[p] = ld16_a4(xa + 4 + 64 * p + 16 * q);
+    for (int k = 0; k < 4; k++) x.a[k] = ld16_a4(xa + 4 + (TYPE == TYPE_Q4_K ? 64 * q + 16 * k : 64 * k + 16 * q));
     x.bs = ld16_a4(xa + 260 + 16 * (q & 1));
 #pragma unroll
     for (int j = 0; j < 4; j++) x.dx[j] = __builtin_bit_cast(float, ld4(xd[j]));
@@ -99,30 +106,29 @@ __device__ __forceinline__ u32x4 mv_funnel(const u32x4& v, uint32_t e, uint32_t 
 
 // The four per-super-block values (tokens 4q + j of row l & 15).
 __device__ __forceinline__ void mv_values(const MvW<TYPE_Q4_K>& w, const MvX& x, int q, float v[4]) {
-    v4i hp[4], lp[4];
+    // planes of the lane's two sub-blocks 2q (low nibbles) and 2q + 1 (high nibbles)
+    const ScMin sm = q4k_scmin_pair(w.hdr.y, w.hdr.z, w.hdr.w, q);
+    const uint32_t al = (sm.sc_lo >> 3) * 0x10001u, bl = (sm.sc_lo & 7u) * 0x10001u;
+    const uint32_t ah = (sm.sc_hi >> 3) * 0x10001u, bh = (sm.sc_hi & 7u) * 0x10001u;
+    const uint32_t ws[8] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w};
+    const uint32_t xw[16] = {x.a[0].x, x.a[0].y, x.a[0].z, x.a[0].w, x.a[1].x, x.a[1].y, x.a[1].z, x.a[1].w,
+                             x.a[2].x, x.a[2].y, x.a[2].z, x.a[2].w, x.a[3].x, x.a[3].y, x.a[3].z, x.a[3].w};
+    v4i hp[4], lp[4], xa[4];
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        const ScMin sm = q4k_scmin_pair(w.hdr.y, w.hdr.z, w.hdr.w, p);
-        const uint32_t sc = (q >> 1) ? sm.sc_hi : sm.sc_lo;          // sub-block 2p + (q >> 1)
-        const uint32_t a2 = (sc >> 3) * 0x10001u, b2 = (sc & 7u) * 0x10001u;
-        const uint32_t ws[4] = {w.qs[p].x, w.qs[p].y, w.qs[p].z, w.qs[p].w};
-        uint32_t hh[4], ll[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t nib = ((q >> 1) ? (ws[i] >> 4) : ws[i]) & 0x0f0f0f0fu;
-            hh[i] = mv_mul_u8x4(nib, a2);
-            ll[i] = mv_mul_u8x4(nib, b2);
-        }
-        hp[p] = v4i{(int)hh[0], (int)hh[1], (int)hh[2], (int)hh[3]};
-        lp[p] = v4i{(int)ll[0], (int)ll[1], (int)ll[2], (int)ll[3]};
+        const uint32_t l0 = ws[2 * p] & 0x0f0f0f0fu, l1 = ws[2 * p + 1] & 0x0f0f0f0fu;
+        const uint32_t h0 = (ws[2 * p] >> 4) & 0x0f0f0f0fu, h1 = (ws[2 * p + 1] >> 4) & 0x0f0f0f0fu;
+        hp[p] = v4i{(int)mv_mul_u8x4(l0, al), (int)mv_mul_u8x4(l1, al), (int)mv_mul_u8x4(h0, ah), (int)mv_mul_u8x4(h1, ah)};
+        lp[p] = v4i{(int)mv_mul_u8x4(l0, bl), (int)mv_mul_u8x4(l1, bl), (int)mv_mul_u8x4(h0, bh), (int)mv_mul_u8x4(h1, bh)};
+        xa[p] = v4i{(int)xw[2 * p], (int)xw[2 * p + 1], (int)xw[8 + 2 * p], (int)xw[9 + 2 * p]};
     }
-    v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[0]), hp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+    v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[0], hp[0], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-    for (int p = 1; p < 4; p++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[p]), hp[p], acc, 0, 0, 0);
+    for (int p = 1; p < 4; p++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[p], hp[p], acc, 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[j] <<= 3;
 #pragma unroll
-    for (int p = 0; p < 4; p++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, x.a[p]), lp[p], acc, 0, 0, 0);
+    for (int p = 0; p < 4; p++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[p], lp[p], acc, 0, 0, 0);
 
     // min term: K 4q..4q+3 = sub-blocks 4(q & 1) .. +3, the high (q < 2) or low part of B
     const ScMin m0 = q4k_scmin_pair(w.hdr.y, w.hdr.z, w.hdr.w, 2 * (q & 1));
@@ -193,8 +199,13 @@ __device__ __forceinline__ void mv_values(const MvW<TYPE_Q6_K>& w, const MvX& x,
 
 // ------------------------------------------------------------------ the kernel
 // Workgroup: 16 rows of one matrix, one wave per chunk of 4 super-blocks (ceil(G/4) <= 16 waves).
-template <int TYPE>
-__global__ void __launch_bounds__(1024)
+// Load schedule of a wave's chunk: with PRE_ALL every super-block's loads are issued before the
+// first is used (four buffers); otherwise two buffers, the next-but-one super-block loaded after
+// each one is used.  SB puts a scheduling barrier behind the initial loads, so that the compiler
+// cannot move the second super-block's loads behind the first one's arithmetic.  LB is the
+// launch bound, which sets the register budget the compiler works to.
+template <int TYPE, int LB, bool PRE_ALL, bool SB>
+__global__ void __launch_bounds__(LB)
 k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float part[16][16][MV_ROWS];            // [chunk][token][row] chunk sums
@@ -221,27 +232,48 @@ k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     }
 
     // the chunk's four super-blocks; columns past G are loaded clamped and contribute +0
-    MvW<TYPE> w[2];
-    MvX x[2];
-    float v[MV_CHUNK][4];
-    auto load = [&](int s, MvW<TYPE>& ww, MvX& xx) {
-        int g = MV_CHUNK * chunk + s;
-        g = g < G ? g : G - 1;
+    const int g0 = MV_CHUNK * chunk;
+    auto wload = [&](int s, MvW<TYPE>& ww) {
+        const int g = g0 + s < G ? g0 + s : G - 1;
         mv_load(ww, wrow + (int64_t)g * col_bytes, q);
+    };
+    auto xload = [&](int s, MvX& xx) {
+        const int g = g0 + s < G ? g0 + s : G - 1;
         const uint8_t* xdg[4] = {xd[0] + g * Q8K_BYTES, xd[1] + g * Q8K_BYTES, xd[2] + g * Q8K_BYTES,
                                  xd[3] + g * Q8K_BYTES};
-        mv_load_x(xx, xa + (int64_t)g * Q8K_BYTES, xdg, q);
+        mv_load_x<TYPE>(xx, xa + (int64_t)g * Q8K_BYTES, xdg, q);
     };
-    load(0, w[0], x[0]);
-    load(1, w[1], x[1]);
-#pragma unroll
-    for (int s = 0; s < MV_CHUNK; s++) {
-        float vv[4];
-        mv_values(w[s & 1], x[s & 1], q, vv);
-        const bool valid = MV_CHUNK * chunk + s < G;
+    float v[MV_CHUNK][4];
+    auto keep = [&](int s, const float (&vv)[4]) {
+        const bool valid = g0 + s < G;
 #pragma unroll
         for (int j = 0; j < 4; j++) v[s][j] = valid ? vv[j] : 0.0f;
-        if (s + 2 < MV_CHUNK) load(s + 2, w[s & 1], x[s & 1]);
+    };
+    if constexpr (PRE_ALL) {
+        MvW<TYPE> w[MV_CHUNK];
+        MvX x[MV_CHUNK];
+#pragma unroll
+        for (int s = 0; s < MV_CHUNK; s++) { wload(s, w[s]); xload(s, x[s]); }
+        if constexpr (SB) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < MV_CHUNK; s++) {
+            float vv[4];
+            mv_values(w[s], x[s], q, vv);
+            keep(s, vv);
+        }
+    } else {
+        MvW<TYPE> w[2];
+        MvX x[2];
+        wload(0, w[0]); xload(0, x[0]);
+        wload(1, w[1]); xload(1, x[1]);
+        if constexpr (SB) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < MV_CHUNK; s++) {
+            float vv[4];
+            mv_values(w[s & 1], x[s & 1], q, vv);
+            keep(s, vv);
+            if (s + 2 < MV_CHUNK) { wload(s + 2, w[s & 1]); xload(s + 2, x[s & 1]); }
+        }
     }
 #pragma unroll
     for (int j = 0; j < 4; j++)
@@ -268,7 +300,18 @@ k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     }
 }
 
-// n (1..3) matrices of one type, N = 1..16 tokens, C <= 16384 (at most 16 chunks of 4 columns).
+template <int TYPE, int LB, bool PRE_ALL, bool SB>
+static void launch_mv(const MvGroup& mg, int wgs, const uint8_t* xq, int N, int G, hipStream_t s) {
+    const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
+    hipLaunchKernelGGL((k_gemv_mfma<TYPE, LB, PRE_ALL, SB>), dim3(wgs), dim3(64 * nchunks), 0, s, mg, xq,
+                       N, G);
+}
+
+// n (1..3) matrices of one type, N = 2..16 tokens, C <= 16384 (at most 16 chunks of 4 columns).
+// Schedules by shape, each the fastest measured for its case (12288x4096 and 4096x12288 Q4_K,
+// 4096x12288 and 1024x4096 Q6_K; N = 3..16):
+//   Q4_K, G <= 16: all four super-blocks in flight (3 waves per SIMD);
+//   Q4_K, G > 16 and Q6_K: two in flight, behind the barrier.
 void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
                             int N, float* const* y, const int64_t* ldy, hipStream_t s) {
     const int G = C / QK;
@@ -283,10 +326,13 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
         wgs += (R[i] + MV_ROWS - 1) / MV_ROWS;
     }
     for (int i = n; i < 4; i++) mg.first[i] = wgs;
-    const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
-    dim3 grid(wgs), block(64 * nchunks);
-    if (type == TYPE_Q4_K) hipLaunchKernelGGL(k_gemv_mfma<TYPE_Q4_K>, grid, block, 0, s, mg, xq, N, G);
-    else hipLaunchKernelGGL(k_gemv_mfma<TYPE_Q6_K>, grid, block, 0, s, mg, xq, N, G);
+    if (type == TYPE_Q4_K) {
+        if (G <= 16) launch_mv<TYPE_Q4_K, 256, true, true>(mg, wgs, xq, N, G, s);
+        else if (G <= 48) launch_mv<TYPE_Q4_K, 768, false, true>(mg, wgs, xq, N, G, s);
+        else launch_mv<TYPE_Q4_K, 1024, false, true>(mg, wgs, xq, N, G, s);
+    } else {
+        launch_mv<TYPE_Q6_K, 1024, false, true>(mg, wgs, xq, N, G, s);
+    }
 }
 
 }  // namespace kq

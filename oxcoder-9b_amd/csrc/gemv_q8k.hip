@@ -43,6 +43,9 @@
 #ifndef KQ_GEMV_MFMA_MIN_N
 #define KQ_GEMV_MFMA_MIN_N 3     // tokens per call from which the MFMA form (gemv_mfma.hip) is used
 #endif
+#ifndef KQ_GEMV_MFMA_MIN_N_Q4_WIDE
+#define KQ_GEMV_MFMA_MIN_N_Q4_WIDE 2   // the same for Q4_K with C > 4096
+#endif
 #ifndef KQ_GEMV_SPLIT_MAX
 #define KQ_GEMV_SPLIT_MAX 4      // most column passes handled by the pass-split kernel (Q4_K)
 #endif
@@ -721,7 +724,8 @@ static void launch1(const MatGroup& mg, const uint8_t* xq, int G, int nt, int rp
 void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s) {
     const int G = C / QK;
-    if (N >= KQ_GEMV_MFMA_MIN_N && G <= 64) {   // 3..16 tokens: the MFMA form (same bits)
+    const int mfma_min = type == TYPE_Q4_K && G > 16 ? KQ_GEMV_MFMA_MIN_N_Q4_WIDE : KQ_GEMV_MFMA_MIN_N;
+    if (N >= mfma_min && G <= 64) {   // the MFMA form (same bits)
         launch_gemv_mfma_group(n, w, R, C, type, xq, N, y, ldy, s);
         return;
     }

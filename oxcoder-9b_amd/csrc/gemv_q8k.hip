@@ -279,8 +279,8 @@ __device__ __forceinline__ void load_act(ActF<TYPE_Q6_K>& a, const float* xg, in
     }
 }
 __device__ __forceinline__ float quad_sum_f32(float v) {
-    v = __fadd_rn(v, __shfl_xor(v, 1, 64));
-    return __fadd_rn(v, __shfl_xor(v, 2, 64));
+    v = __fadd_rn(v, dppf<DPP_QUAD_XOR1>(v));
+    return __fadd_rn(v, dppf<DPP_QUAD_XOR2>(v));
 }
 __device__ __forceinline__ float block_value(const Frag<TYPE_Q4_K>& f, const ActF<TYPE_Q4_K>& a, int p) {
     const ScMin sm = q4k_scmin_pair(f.hdr.y, f.hdr.z, f.hdr.w, p);

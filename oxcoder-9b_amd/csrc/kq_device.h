@@ -99,7 +99,38 @@ constexpr int DPP_QUAD_XOR1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int DPP_ROW_HALF_MIRROR = 0x141; // lane j of each 8 <- lane 7-j
 constexpr int DPP_ROW_MIRROR = 0x140;      // lane j of each 16 <- lane 15-j
-constexpr int SWZ_XOR16 = (0x10 << 10) | 0x1F;  // ds_swizzle bit mode: lane ^ 16
+
+// Partner values across 16- and 32-lane distances with the gfx950 permlane swaps (VALU, no LDS
+// round trip).  With both operands v, v_permlane16_swap returns rows (0, 0, 2, 2) of v in one
+// result and rows (1, 1, 3, 3) in the other; v_permlane32_swap returns halves (0, 0) and (1, 1).
+// Lane i therefore holds {v[i], v[i ^ 16]} (resp. {v[i], v[i ^ 32]}) in the two results, in an
+// order that depends on i; fp32 addition and fmax are commutative, so the butterfly sum or max of
+// the pair has the same bits in either order.
+struct LanePair { uint32_t a, b; };
+__device__ __forceinline__ LanePair xor16_pair(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return LanePair{r[0], r[1]};
+}
+__device__ __forceinline__ LanePair xor32_pair(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return LanePair{r[0], r[1]};
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+    const LanePair r = xor16_pair(__builtin_bit_cast(uint32_t, v));
+    return __fadd_rn(__builtin_bit_cast(float, r.a), __builtin_bit_cast(float, r.b));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const LanePair r = xor32_pair(__builtin_bit_cast(uint32_t, v));
+    return __fadd_rn(__builtin_bit_cast(float, r.a), __builtin_bit_cast(float, r.b));
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const LanePair r = xor16_pair(__builtin_bit_cast(uint32_t, v));
+    return __builtin_fmaxf(__builtin_bit_cast(float, r.a), __builtin_bit_cast(float, r.b));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const LanePair r = xor32_pair(__builtin_bit_cast(uint32_t, v));
+    return __builtin_fmaxf(__builtin_bit_cast(float, r.a), __builtin_bit_cast(float, r.b));
+}
 
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
@@ -117,12 +148,13 @@ __device__ __forceinline__ int quad_sum_i32(int v) {
 }
 // Pairwise tree over the 16 super-block slots held by lane bits 2..5 (slot = lane >> 2), for a
 // value that is uniform within each quad: ((s0+s1)+(s2+s3)) + ... in natural slot order.
-// Within a 16-lane row the mirrors pair quad 0 with 1 and 2 with 3, then the two halves.
+// Within a 16-lane row the mirrors pair quad 0 with 1 and 2 with 3, then the two halves; then
+// the rows (lane ^ 16) and the halves of the wave (lane ^ 32).
 __device__ __forceinline__ float slot_tree_f32(float v) {
     v = __fadd_rn(v, dppf<DPP_ROW_HALF_MIRROR>(v));
     v = __fadd_rn(v, dppf<DPP_ROW_MIRROR>(v));
-    v = __fadd_rn(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), SWZ_XOR16)));
-    return __fadd_rn(v, __shfl_xor(v, 32, 64));
+    v = xor16_sum(v);
+    return xor32_sum(v);
 }
 
 }  // namespace kq

@@ -21,8 +21,8 @@ __device__ __forceinline__ void q8k_block_store(const float (&e)[4], int lane, u
     amax = __builtin_fmaxf(amax, dppf<DPP_QUAD_XOR2>(amax));
     amax = __builtin_fmaxf(amax, dppf<DPP_ROW_HALF_MIRROR>(amax));
     amax = __builtin_fmaxf(amax, dppf<DPP_ROW_MIRROR>(amax));
-    amax = __builtin_fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, amax), SWZ_XOR16)));
-    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, 64));
+    amax = xor16_max(amax);
+    amax = xor32_max(amax);
     // signed value of the first element with |x| == amax: lowest lane holding one, lowest k in it
     float first = 0.0f;
     bool has = false;

@@ -154,19 +154,40 @@ __device__ __forceinline__ void load_frag(Frag<TYPE_Q6_K>& f, const uint8_t* bk,
 //   l0 of p = 0, 1, 2, 3 (offsets 16, 32, 80, 96) is l0.x of lane 1, l1.x of lane 0, l0.x of lane 3, l1.x of lane 2;
 //   l1 (offsets 48, 64, 112, 128) is l1.x of lane 1, l0.x of lane 2, l1.x of lane 3, hb.x of lane 0;
 //   hb (offsets 144, 160, 176, 192) is hb.x of lanes 1, 2, 3 and, for p = 3, the first scale dword.
+// Lane-dependent choice between two words as a bit select.
+__device__ __forceinline__ uint32_t pick(bool c, uint32_t a, uint32_t b) {
+    const uint32_t m = 0u - (uint32_t)c;
+    return (a & m) | (b & ~m);
+}
+// SEL: the lane-dependent choices as bit selects.  Written as conditional expressions the compiler
+// turns them into divergent branches with exec-mask bookkeeping; the bit selects measured faster
+// in the pass-split kernel (1024x4096 Q6_K 4.03 -> 3.77 us) and for two tokens (4096x12288 Q6_K
+// 12.6 -> 11.8 us), slower in the one-token three-pass kernel (10.6 -> 11.2 us, with earlier waits
+// on the weight loads in flight), which keeps the branches.  The fields are the same either way.
+template <bool SEL = true>
 __device__ __forceinline__ Q6Fields prepare(const Frag<TYPE_Q6_K>& f, int p) {
     constexpr int QUAD_ROT1 = 0x39;   // quad_perm [1,2,3,0]: lane i <- lane (i + 1) & 3
     const int h = p >> 1, jj = p & 1;
     Q6Fields q;
     q.l0 = f.l0; q.l1 = f.l1; q.hb = f.hb; q.dw = f.dw; q.sh = f.sh;
-    q.l0e = (uint32_t)dpp<DPP_QUAD_XOR1>((int)(jj ? f.l0.x : f.l1.x));
-    q.l1e = (uint32_t)dpp<QUAD_ROT1>((int)(p == 0 ? f.hb.x : (p == 2 ? f.l0.x : f.l1.x)));
-    const uint32_t hn = (uint32_t)dpp<QUAD_ROT1>((int)f.hb.x);
-    q.hbe = p == 3 ? f.sc4.x : hn;
-    q.sc = h ? u32x2{f.sc4.z, f.sc4.w} : u32x2{f.sc4.x, f.sc4.y};   // scales 8h .. 8h+7
-    q.sce = h ? f.dw : f.sc4.z;                                     // the dword after them
+    if constexpr (SEL) {
+        q.l0e = (uint32_t)dpp<DPP_QUAD_XOR1>((int)pick(jj, f.l0.x, f.l1.x));
+        q.l1e = (uint32_t)dpp<QUAD_ROT1>((int)pick(p == 0, f.hb.x, pick(p == 2, f.l0.x, f.l1.x)));
+        const uint32_t hn = (uint32_t)dpp<QUAD_ROT1>((int)f.hb.x);
+        q.hbe = pick(p == 3, f.sc4.x, hn);
+        q.sc = u32x2{pick(h, f.sc4.z, f.sc4.x), pick(h, f.sc4.w, f.sc4.y)};   // scales 8h .. 8h+7
+        q.sce = pick(h, f.dw, f.sc4.z);                                       // the dword after them
+    } else {
+        q.l0e = (uint32_t)dpp<DPP_QUAD_XOR1>((int)(jj ? f.l0.x : f.l1.x));
+        q.l1e = (uint32_t)dpp<QUAD_ROT1>((int)(p == 0 ? f.hb.x : (p == 2 ? f.l0.x : f.l1.x)));
+        const uint32_t hn = (uint32_t)dpp<QUAD_ROT1>((int)f.hb.x);
+        q.hbe = p == 3 ? f.sc4.x : hn;
+        q.sc = h ? u32x2{f.sc4.z, f.sc4.w} : u32x2{f.sc4.x, f.sc4.y};
+        q.sce = h ? f.dw : f.sc4.z;
+    }
     return q;
 }
+template <bool SEL = true>
 __device__ __forceinline__ const Frag<TYPE_Q4_K>& prepare(const Frag<TYPE_Q4_K>& f, int) { return f; }
 __device__ __forceinline__ u32x4 funnel(const u32x4& v, uint32_t e, uint32_t sh) {
     u32x4 r;
@@ -529,7 +550,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
                 const bool valid = slot + 16 * PS < G;
 #pragma unroll
                 for (int r = 0; r < RPW; r++) {
-                    const auto fr = prepare(cur[r], p);
+                    const auto fr = prepare<false>(cur[r], p);
 #pragma unroll
                     for (int t = 0; t < NT; t++) {
                         const float v = block_value(fr, actp[PS][t], p);

@@ -525,7 +525,8 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
         using I2 = std::integral_constant<int, 2>;
         if constexpr (NT == 1 && KQ_GEMV_SEQ_DEPTH == 2) {
             // two steps in flight: step i issues the loads of step i + 2 into the buffer step i - 1 used
-            // (one token: 4096x12288 Q6_K 11.6 -> 11.1 us; two tokens were slower with it)
+            // (one token: 4096x12288 Q6_K 11.6 -> 11.1 us; two tokens were slower with it, and three
+            // steps in flight slower again: 10.6 -> 11.5 us)
             Frag<TYPE> bufC[RPW];
 #pragma unroll
             for (int r = 0; r < RPW; r++) load_frag(bufB[r], base + (int64_t)(slot + 16 < G ? slot + 16 : G - 1) * col_bytes + r * BS, p);

@@ -230,8 +230,10 @@ __device__ __forceinline__ float block_value(const Frag<TYPE_Q4_K>& f, const Act
     const ScMin sm = q4k_scmin_pair(f.hdr.y, f.hdr.z, f.hdr.w, p);
     int plo, phi;
     q4k_lane_dots(f.qa, f.qb, a.xl, a.xh, plo, phi);
-    const int i1 = quad_sum_i32((int)sm.sc_lo * plo + (int)sm.sc_hi * phi);
-    const int i2 = quad_sum_i32((int)sm.m_lo * a.blo + (int)sm.m_hi * a.bhi);
+    // 24-bit multiplies (v_mul_i32_i24 / v_mad_i32_i24, full rate; the 32-bit v_mul_lo_u32 is quarter
+    // rate): scales and mins < 64, |plo|, |phi| <= 32*15*128, |blo|, |bhi| <= 32*127, products exact
+    const int i1 = quad_sum_i32(__mul24((int)sm.sc_lo, plo) + __mul24((int)sm.sc_hi, phi));
+    const int i2 = quad_sum_i32(__mul24((int)sm.m_lo, a.blo) + __mul24((int)sm.m_hi, a.bhi));
     return q4k_value(f.hdr.x, a.dx, i1, i2);
 }
 __device__ __forceinline__ float block_value(const Q6Fields& f, const Act<TYPE_Q6_K>& a, int p) {
@@ -240,10 +242,11 @@ __device__ __forceinline__ float block_value(const Q6Fields& f, const Act<TYPE_Q
     const uint32_t w1 = __builtin_amdgcn_alignbyte(f.sce, f.sc.y, f.sh);    // scales 8h+4 .. 8h+7
     int P[4];
     q6k_lane_dots(funnel(f.l0, f.l0e, f.sh), funnel(f.l1, f.l1e, f.sh), funnel(f.hb, f.hbe, f.sh), a.xa, P);
-    int I = sbyte(w0, jj) * (P[0] - a.corr[0]);
-    I += sbyte(w0, jj + 2) * (P[1] - a.corr[1]);
-    I += sbyte(w1, jj) * (P[2] - a.corr[2]);
-    I += sbyte(w1, jj + 2) * (P[3] - a.corr[3]);
+    // 24-bit multiplies: |scale| <= 128, |P - corr| <= 16*63*127 + 32*16*127, products exact
+    int I = __mul24(sbyte(w0, jj), P[0] - a.corr[0]);
+    I += __mul24(sbyte(w0, jj + 2), P[1] - a.corr[1]);
+    I += __mul24(sbyte(w1, jj), P[2] - a.corr[2]);
+    I += __mul24(sbyte(w1, jj + 2), P[3] - a.corr[3]);
     I = quad_sum_i32(I);
     return q6k_value(f16_lo(f.dw >> (8 * f.sh)), a.dx, I);
 }

@@ -65,7 +65,7 @@ template <> struct MvW<TYPE_Q6_K> { u32x4 ql[2], qh[2], sc; uint32_t qle[2], qhe
 
 struct MvX {
     u32x4 a[4];     // activation bytes of token l & 15: Q4_K 64q + 16k .. +15, Q6_K 64k + 16q .. +15
-    u32x4 bs;       // bsums 8(q & 1) .. 8(q & 1) + 7 of token l & 15 (Q4_K min term)
+    u32x4 bs;       // bsums 8(q & 1) .. 8(q & 1) + 7 of token l & 15 (Q4_K min term; not loaded for Q6_K)
     float dx[4];    // d of tokens 4q + j
 };
 
@@ -94,7 +94,7 @@ template <int TYPE>
 __device__ __forceinline__ void mv_load_x(MvX& x, const uint8_t* xa, const uint8_t* const* xd, int q) {
 #pragma unroll
     for (int k = 0; k < 4; k++) x.a[k] = ld16_a4(xa + 4 + (TYPE == TYPE_Q4_K ? 64 * q + 16 * k : 64 * k + 16 * q));
-    x.bs = ld16_a4(xa + 260 + 16 * (q & 1));
+    if constexpr (TYPE == TYPE_Q4_K) x.bs = ld16_a4(xa + 260 + 16 * (q & 1));   // the min term's bsums
 #pragma unroll
     for (int j = 0; j < 4; j++) x.dx[j] = __builtin_bit_cast(float, ld4(xd[j]));
 }

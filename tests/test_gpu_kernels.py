@@ -201,10 +201,12 @@ def test_batched_reference_inputs_bit_identical(dev, orc, ty):
     assert_close_inf(host(yb), orc.gemv_q8k(W, R, C, ty, xq, 7))
 
 
-@pytest.mark.parametrize("N", [1, 3, 6])
-def test_gemv_q8k_multi_matches_single(dev, orc, N):
-    """q/k/v-style group (two Q4_K, one Q6_K) in one call equals three single calls bit for bit."""
-    C = 4096
+@pytest.mark.parametrize("C,N", [(4096, 1), (4096, 3), (4096, 6), (12288, 2), (12288, 4)])
+def test_gemv_q8k_multi_matches_single(dev, orc, C, N):
+    """q/k/v-style group (two Q4_K, one Q6_K) in one call equals three single calls bit for bit; at
+    C = 12288 and two tokens the Q4_K matrices take the MFMA kernel and the Q6_K one the v_dot4 GEMV
+    within the same call."""
+    print("multi", C, N, flush=True)
     mats_h = [(synth(R, C, ty, 50 + i), R, C, ty) for i, (R, ty) in enumerate([(4096, 12), (1024, 12), (1024, 14)])]
     mats = [(dev_t(W, dev), R, C_, ty) for (W, R, C_, ty) in mats_h]
     xq = orc.quantize_q8k(kqq.synthetic_activations(N, C, seed=N))

@@ -49,6 +49,13 @@
 #ifndef KQ_GEMV_MFMA_MIN_N_Q4_WIDE
 #define KQ_GEMV_MFMA_MIN_N_Q4_WIDE 2   // the same for Q4_K with C > 4096
 #endif
+// The MFMA form runs one workgroup per 16 rows; below this many rows in a call (fewer than 256
+// workgroups) it leaves CUs idle, and up to 4 tokens the v_dot4 kernels are faster there (N = 3 / 4:
+// 1024x4096 Q6_K 6.8 / 6.9 -> 4.7 / 5.5 us, 2048x12288 Q6_K 13.9 / 14.1 -> 10.9 / 12.7 us, 1024x4096
+// Q4_K 5.2 / 5.3 -> 4.3 / 5.1 us; from 4096 rows the MFMA form is as fast or faster at N = 4).
+#ifndef KQ_GEMV_MFMA_MIN_ROWS
+#define KQ_GEMV_MFMA_MIN_ROWS 4096
+#endif
 #ifndef KQ_GEMV_SPLIT_MAX
 #define KQ_GEMV_SPLIT_MAX 4      // most column passes handled by the pass-split kernel (Q4_K)
 #endif
@@ -810,7 +817,10 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s) {
     const int G = C / QK;
     const int mfma_min = type == TYPE_Q4_K && G > 16 ? KQ_GEMV_MFMA_MIN_N_Q4_WIDE : KQ_GEMV_MFMA_MIN_N;
-    if (N >= mfma_min && G <= 64) {   // the MFMA form (same bits)
+    int rows = 0;
+    for (int i = 0; i < n; i++) rows += R[i];
+    const bool few_rows = N <= 4 && rows < KQ_GEMV_MFMA_MIN_ROWS;
+    if (N >= mfma_min && G <= 64 && !few_rows) {   // the MFMA form (same bits)
         launch_gemv_mfma_group(n, w, R, C, type, xq, N, y, ldy, s);
         return;
     }

@@ -102,11 +102,13 @@ def test_gemm_exact(dev, orc, ty, R, C, M, amp):
     assert_exact(host(y2), ref, "kq_gemm_q8k")
 
 
-@pytest.mark.parametrize("ty,R,C,amp", [(12, 4096, 4096, 3), (14, 4096, 4096, 3), (12, 1024, 12288, 1),
-                                        (14, 1024, 12288, 1), (12, 64, 16640, 1), (14, 40, 16640, 1)])
+@pytest.mark.parametrize("ty,R,C,amp", [(12, 4096, 4096, 3), (14, 4096, 4096, 3), (12, 4096, 12288, 1),
+                                        (12, 1024, 12288, 1), (14, 1024, 12288, 1), (12, 64, 16640, 1),
+                                        (14, 40, 16640, 1)])
 def test_gemv_batches_exact(dev, orc, ty, R, C, amp):
-    """N = 1, 2 (v_dot4 GEMV; Q4_K with 4096 < C <= 16384 takes the MFMA planes from N = 2) and
-    N = 3..16 (int8 MFMA planes, and beyond 16384 columns the v_dot4 kernel again): every row exact."""
+    """N = 1, 2 (v_dot4 GEMV; Q4_K with 4096 < C <= 16384 and at least 4096 rows takes the MFMA
+    planes from N = 2), N = 3, 4 (MFMA planes from 4096 rows, v_dot4 below) and N = 8, 16 (MFMA
+    planes; beyond 16384 columns the v_dot4 kernel again): every row exact."""
     print("gemv exact", ty, R, C, flush=True)
     W, X, xq, ref = prepare(orc, R, C, ty, 16, seed=R + C + 7, amp=amp)
     wd, xqd = dev_t(W, dev), dev_t(xq, dev)

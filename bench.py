@@ -667,6 +667,47 @@ def decode_stream_extra(torch, rn, dev):
             "hbm_frac": round(total / el / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def tp_shard_extra(torch, rn, dev, tp=8, copies=64):
+    """One GPU's share of the decode layer under tensor parallelism over `tp` GPUs, at its real
+    shapes: column-parallel q, k, v, gate, up keep R/tp rows; row-parallel o and down keep C/tp
+    columns (their partial outputs would then be all-reduced, which one GPU cannot show).  Same
+    step structure as the headline (4 quantizations, shared-input matrices in one launch), `copies`
+    resident shard copies, graph-replayed."""
+    from kq import quantize as kqq
+    cols = [4096, 4096 // tp, 4096, 12288 // tp]
+    shard = []
+    for name, R, C_, ty, slot in LAYER:
+        if name in ("attn_output", "ffn_down"):
+            shard.append((name, R, C_ // tp, ty, slot))
+        else:
+            shard.append((name, R // tp, C_, ty, slot))
+    base = {name: torch.from_numpy(kqq.synthetic_matrix(R, C_, ty, seed=200 + i)).to(dev)
+            for i, (name, R, C_, ty, _) in enumerate(shard)}
+    lays = [base] + [{k: v.clone() for k, v in base.items()} for _ in range(copies - 1)]
+    xs = [torch.from_numpy(kqq.synthetic_activations(1, c, seed=s)[0]).to(dev) for s, c in enumerate(cols)]
+    xqs = [torch.empty((c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in cols]
+    ys = {name: torch.empty(R, device=dev) for name, R, _, _, _ in shard}
+
+    def fn():
+        s = rn.stream()
+        for lay in lays:
+            for slot, c in enumerate(cols):
+                rn.quantize(xs[slot], c, xqs[slot], s)
+                group = [(n, R, C2, ty) for n, R, C2, ty, sl in shard if sl == slot]
+                rn.gemv_multi([(lay[n], R, C2, ty) for n, R, C2, ty in group], xqs[slot], [ys[n] for n, *_ in group], s)
+
+    g = capture(torch, fn)
+    time_graphs(torch, [g])
+    reps = 10
+    per = time_graphs(torch, [g] * reps) / (reps * copies)
+    nbytes = sum(wbytes(R, C_, ty) + (C_ // 256) * Q8K + R * 4 for _, R, C_, ty, _ in shard)
+    nbytes += sum(c * 4 + (c // 256) * Q8K for c in cols)
+    del lays, base
+    return {"tp": tp, "shapes": {n: "%dx%d %s" % (R, C_, "Q4_K" if ty == 12 else "Q6_K") for n, R, C_, ty, _ in shard},
+            "bytes_per_step": nbytes, "us_per_step": round(per * 1e6, 2), "GB/s": round(nbytes / per / 1e9, 1),
+            "launches_per_step": 8}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -675,7 +716,8 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
-    ap.add_argument("--only", choices=("batched", "producers", "f32_layer", "gemm", "head", "decode_stream", "pack"),
+    ap.add_argument("--only", choices=("batched", "producers", "f32_layer", "gemm", "head", "decode_stream", "pack",
+                                       "tp_shard"),
                     help="run only this extra (no headline step, no CPU baseline) and print its JSON; for "
                          "profiling one workload")
     ap.add_argument("--pmc-workload", choices=("gemv", "gemm", "q6k"),
@@ -710,7 +752,8 @@ def main():
               "gemm": lambda: gemm_extra(torch, rn, dev),
               "head": lambda: head_extra(torch, rn, dev),
               "decode_stream": lambda: decode_stream_extra(torch, rn, dev),
-              "pack": lambda: pack_extra(torch, dev)}[a.only]
+              "pack": lambda: pack_extra(torch, dev),
+              "tp_shard": lambda: tp_shard_extra(torch, rn, dev)}[a.only]
         print(json.dumps({a.only: fn()}), flush=True)
         return
     log("bench: building %d resident layer copies" % a.copies)
@@ -789,6 +832,8 @@ def main():
         result["decode_stream"] = decode_stream_extra(torch, rn, dev)
         log("bench: pack loading")
         result["pack_load"] = pack_extra(torch, dev)
+        log("bench: one GPU's share of the layer at TP8")
+        result["tp8_shard_layer"] = tp_shard_extra(torch, rn, dev)
     if not a.no_cpu:
         log("bench: CPU baseline")
         result["cpu_baseline"] = cpu_baseline()

@@ -592,14 +592,14 @@ def head_extra(torch, rn, dev):
 
 
 def gemm_extra(torch, rn, dev, timed=True):
-    """Prefill GEMM: M in {128, 512, 2048} (128: a prefill chunk, where K is split); 12288x4096 Q4_K
-    and 4096x12288 Q6_K (timed=False: two direct calls per shape at M = 512 and 2048, for counter
-    runs)."""
+    """Prefill GEMM: M in {128, 256, 512, 2048} (256: the Engine's prefill chunk, KINDI_CHUNK; at 128
+    and 256 K is split where the tiles are too few); 12288x4096 Q4_K and 4096x12288 Q6_K (timed=False:
+    two direct calls per shape at M = 512 and 2048, for counter runs)."""
     from kq import ops, quantize as kqq
     out = {}
     for name, R, C_, ty in (("gate_12288x4096_q4k", 12288, 4096, 12), ("down_4096x12288_q6k", 4096, 12288, 14)):
         w = torch.from_numpy(kqq.synthetic_matrix(R, C_, ty, seed=60 + ty)).to(dev)
-        for M in ((128, 512, 2048) if timed else (512, 2048)):
+        for M in ((128, 256, 512, 2048) if timed else (512, 2048)):
             X = torch.from_numpy(kqq.synthetic_activations(M, C_, seed=M)).to(dev)
             xq = ops.q8k_quantize(X)
             y = torch.empty((M, R), device=dev)

@@ -667,6 +667,50 @@ def decode_stream_extra(torch, rn, dev):
             "hbm_frac": round(total / el / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def prefill_chunk_extra(torch, rn, dev, layers, M=256):
+    """One prefill chunk of M tokens (the Engine's KINDI_CHUNK) through a decode layer's 7 matrices, as
+    Engine.gemm runs it: each of the 4 inputs quantized once (M rows), then the matrices sharing it
+    in one kq_gemm_q8k_multi_ws call (one fragment copy, one GEMM launch); beside it the same chunk
+    with one kq_gemm_q8k_ws call per matrix.  The resident layer copies rotate."""
+    from kq import ops, quantize as kqq
+    xs = [torch.from_numpy(kqq.synthetic_activations(M, c, seed=10 + s)).to(dev) for s, c in enumerate(INPUT_COLS)]
+    xqs = [torch.empty(M * (c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
+    ys = {name: torch.empty((M, R), device=dev) for name, R, _, _, _ in LAYER}
+    groups = [[(n, R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == slot] for slot in range(len(INPUT_COLS))]
+    need = max(ops.gemm_multi_workspace_bytes([R for _, R, _, _ in g], g[0][2], M) for g in groups)
+    ws = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+    wsa = ws[(-ws.data_ptr()) % 256:]
+    copies = min(len(layers), 8)
+
+    def run(grouped):
+        def fn():
+            s = rn.stream()
+            for lay in layers[:copies]:
+                for slot, c in enumerate(INPUT_COLS):
+                    rn.check(rn.lib.kq_q8k_quantize(C.c_void_p(xs[slot].data_ptr()), c, c, M,
+                                                    C.c_void_p(xqs[slot].data_ptr()), s))
+                    if grouped:
+                        ops.gemm_q8k_multi([(lay[n], R, C2, ty) for n, R, C2, ty in groups[slot]], xqs[slot], M,
+                                           [ys[n] for n, *_ in groups[slot]], ws)
+                    else:
+                        for n, R, C2, ty in groups[slot]:
+                            rn.gemm(lay[n], R, C2, ty, xqs[slot], M, ys[n], wsa, s)
+
+        g = capture(torch, fn)
+        warm = 0.0
+        while warm < 0.2:
+            warm += time_graphs(torch, [g])
+        reps = 5
+        return time_graphs(torch, [g] * reps) / (reps * copies)
+
+    per = run(True)
+    per_single = run(False)
+    ops_ = sum(2 * M * R * C_ for _, R, C_, _, _ in LAYER)
+    return {"tokens": M, "us_per_layer": round(per * 1e6, 1), "tokens_per_s_per_layer": round(M / per, 1),
+            "TOPS": round(ops_ / per / 1e12, 1), "frac_int8_peak": round(ops_ / per / 1e12 / INT8_PEAK_TOPS, 4),
+            "one_call_per_matrix_us": round(per_single * 1e6, 1)}
+
+
 def tp_shard_extra(torch, rn, dev, tp=8, copies=64):
     """One GPU's share of the decode layer under tensor parallelism over `tp` GPUs, at its real
     shapes: column-parallel q, k, v, gate, up keep R/tp rows; row-parallel o and down keep C/tp
@@ -717,7 +761,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
     ap.add_argument("--only", choices=("batched", "producers", "f32_layer", "gemm", "head", "decode_stream", "pack",
-                                       "tp_shard"),
+                                       "tp_shard", "prefill_chunk"),
                     help="run only this extra (no headline step, no CPU baseline) and print its JSON; for "
                          "profiling one workload")
     ap.add_argument("--pmc-workload", choices=("gemv", "gemm", "q6k"),
@@ -744,7 +788,7 @@ def main():
         pmc_workload_q6k(torch, rn, dev)
         return
     if a.only:
-        need_layers = a.only in ("producers", "f32_layer")
+        need_layers = a.only in ("producers", "f32_layer", "prefill_chunk")
         lay = make_layer(torch, dev, a.copies) if need_layers else None
         fn = {"batched": lambda: batched_extra(torch, rn, dev, 160),
               "producers": lambda: producers_extra(torch, rn, lay, dev),
@@ -753,7 +797,8 @@ def main():
               "head": lambda: head_extra(torch, rn, dev),
               "decode_stream": lambda: decode_stream_extra(torch, rn, dev),
               "pack": lambda: pack_extra(torch, dev),
-              "tp_shard": lambda: tp_shard_extra(torch, rn, dev)}[a.only]
+              "tp_shard": lambda: tp_shard_extra(torch, rn, dev),
+              "prefill_chunk": lambda: prefill_chunk_extra(torch, rn, dev, lay)}[a.only]
         print(json.dumps({a.only: fn()}), flush=True)
         return
     log("bench: building %d resident layer copies" % a.copies)
@@ -824,6 +869,8 @@ def main():
         result["f32_layer"] = f32_layer_extra(torch, rn, layers, dev)
         log("bench: prefill GEMM")
         result["prefill_gemm"] = gemm_extra(torch, rn, dev)
+        log("bench: prefill chunk through a layer")
+        result["prefill_chunk_layer"] = prefill_chunk_extra(torch, rn, dev, layers)
         del layers
         torch.cuda.empty_cache()
         log("bench: output head")

@@ -167,6 +167,20 @@ int kq_gemm_q8k_ws(const void* w, int R, int C, int type, const void* xq, int M,
                    int64_t ldy, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * Up to 3 matrices sharing one Q8_K input (q/k/v, gate/up of a prefill chunk): the prefill GEMM of
+ * each, with one fragment copy of the activations for all of them and one GEMM launch per weight
+ * type, so the small matrices' tiles fill the GPU together.  The chunked prefill runs one GEMM per
+ * projection on each chunk's shared input (chunk.py:165-177, ternary k_mm_g5q chunk.cu:820); the
+ * reference's GPU operator takes several matrices on one input the same way
+ * (Engine.gemv(names, x, outs), gpu4.py:95-99).  C and M are common; R[i], type[i], y[i] and
+ * ldy[i] per matrix.  ws (256-byte aligned) holds kq_gemm_q8k_multi_workspace(n, R, C, M) bytes.
+ * Every y[i] equals what kq_gemm_q8k_ws gives for that matrix alone, bit for bit.
+ */
+size_t kq_gemm_q8k_multi_workspace(int n, const int* R, int C, int M);
+int kq_gemm_q8k_multi_ws(int n, const void* const* w, const int* R, int C, const int* type, const void* xq, int M,
+                         float* const* y, const int64_t* ldy, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * kq_gemm_q8k_ws without a caller workspace and without any allocation: the workspace is the
  * library's static device array of KQ_GEMM_STATIC_SCRATCH_BYTES (one per device, held until the
  * process ends; a 256-token prefill chunk of every 9B-model matrix fits).  No counterpart in the

@@ -268,6 +268,29 @@ int kq_gemm_q8k_ws(const void* w, int R, int C, int type, const void* xq, int M,
     return check_launch(fn);
 }
 
+size_t kq_gemm_q8k_multi_workspace(int n, const int* R, int C, int M) {
+    if (n < 1 || n > 3 || !R || C < 256 || C % 256 || M < 1) return 0;
+    for (int i = 0; i < n; i++)
+        if (R[i] < 8 || R[i] % 8) return 0;
+    return gemm_q8k_group_workspace(n, R, C, M);
+}
+
+int kq_gemm_q8k_multi_ws(int n, const void* const* w, const int* R, int C, const int* type, const void* xq, int M,
+                         float* const* y, const int64_t* ldy, void* ws, size_t ws_bytes, void* stream) {
+    static const char* fn = "kq_gemm_q8k_multi_ws";
+    if (n < 1 || n > 3) return fail(KQ_ERR_ARG, "%s: n=%d must be 1..3", fn, n);
+    if (!w || !R || !type || !y || !ldy) return fail(KQ_ERR_ARG, "%s: NULL array argument", fn);
+    for (int i = 0; i < n; i++) KQ_TRY(check_gemm(w[i], R[i], C, type[i], xq, M, y[i], ldy[i], fn));
+    KQ_TRY(check_ptr(ws, 256, "ws", fn));
+    const size_t need = gemm_q8k_group_workspace(n, R, C, M);
+    if (ws_bytes < need) return fail(KQ_ERR_ARG, "%s: workspace of %zu bytes, %zu needed", fn, ws_bytes, need);
+    const uint8_t* wb[3];
+    for (int i = 0; i < n; i++) wb[i] = static_cast<const uint8_t*>(w[i]);
+    launch_gemm_q8k_group(n, wb, R, C, type, static_cast<const uint8_t*>(xq), M, y, ldy, static_cast<uint8_t*>(ws),
+                          as_stream(stream));
+    return check_launch(fn);
+}
+
 int kq_gemm_q8k_static(const void* w, int R, int C, int type, const void* xq, int M, float* y,
                        int64_t ldy, void* stream) {
     static const char* fn = "kq_gemm_q8k_static";

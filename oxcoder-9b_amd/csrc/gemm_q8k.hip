@@ -37,10 +37,14 @@
 // and not stored.
 //
 // K split.  When the output tiles are too few to fill the GPU (small M, or few weight rows), each
-// tile is computed by S workgroups (grid z), each over a contiguous range of super-blocks, into
-// S partial planes of the workspace; k_gemm_reduce then adds the planes in order s = 0, 1, ...
-// The split depends only on (R, C, M), so results are deterministic; it needs the workspace, so
-// kq_gemm_q8k (no workspace) never splits.
+// tile is computed by S workgroups, each over a contiguous range of super-blocks, into S partial
+// planes of the workspace; k_gemm_reduce then adds the planes in order s = 0, 1, ...  The split
+// depends only on (R, C, M), so results are deterministic; it needs the workspace, so kq_gemm_q8k
+// (no workspace) never splits.
+//
+// Matrices sharing the activations (q/k/v, gate/up) can go in one call: one fragment copy, and one
+// GEMM launch per weight type whose grid holds every matrix's tiles (and splits), so that small
+// matrices fill the GPU together; each matrix keeps its own split, so its results do not change.
 #include <atomic>
 #include <mutex>
 #include <type_traits>
@@ -275,14 +279,28 @@ __device__ __forceinline__ void stage_x(const RawX<XP>& r, int mr, int xp, GemmB
 }
 
 // ------------------------------------------------------------------ the kernel
+// One launch covers up to three matrices of one type that share the activations (q/k/v, gate/up):
+// workgroup x = wg0 of its matrix + split * ntile + weight tile (weight tile fastest), y = token
+// tile.  Each matrix keeps the K split a call of its own would take, so its results are those of
+// that call bit for bit.
+struct GemmMat {
+    const uint8_t* w;
+    float* y;
+    float* part;      // partial planes of the K split (S of M x R floats), or null
+    int64_t ldy;
+    int R, ntile, gps, wg0;
+};
+struct GemmGroup {
+    GemmMat m[3];
+    int n;
+};
+
 // WN waves along n times WM along m; each wave owns 64 tokens x 32 weight rows (two 32x32 MFMA
 // tiles), the workgroup BM = 64*WM tokens x BN = 32*WN rows.  FRAG: A operands from the
 // fragment-order copy XF, else straight from the Q8_K rows XQ.
 template <int TYPE, int BN, int WN, int WM, bool FRAG>
 __global__ void __launch_bounds__(64 * WN * WM)
-k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restrict__ XQ,
-           const uint8_t* __restrict__ XF, int M, float* __restrict__ Y, int64_t ldy, int gps,
-           float* __restrict__ P, int64_t pstride) {
+k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* __restrict__ XF, int M) {
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     constexpr int BM = 64 * WM;
     constexpr int NTHR = 64 * WN * WM;
@@ -299,12 +317,25 @@ k_gemm_q8k(const uint8_t* __restrict__ W, int R, int G, const uint8_t* __restric
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % WM, wn = wave / WM;
     const int half = lane >> 5, l32 = lane & 31;
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    // this workgroup's matrix (the argument fields picked by selects on the wave-uniform index)
+    const int bx = blockIdx.x;
+    const int mi = gg.n > 1 && bx >= gg.m[1].wg0 ? (gg.n > 2 && bx >= gg.m[2].wg0 ? 2 : 1) : 0;
+    auto field = [&](auto get) { return mi == 0 ? get(gg.m[0]) : mi == 1 ? get(gg.m[1]) : get(gg.m[2]); };
+    const uint8_t* const W = field([](const GemmMat& g) { return g.w; });
+    float* const Y = field([](const GemmMat& g) { return g.y; });
+    float* const P = field([](const GemmMat& g) { return g.part; });
+    const int64_t ldy = field([](const GemmMat& g) { return g.ldy; });
+    const int R = field([](const GemmMat& g) { return g.R; });
+    const int ntile = field([](const GemmMat& g) { return g.ntile; });
+    const int gps = field([](const GemmMat& g) { return g.gps; });
+    const int local = bx - field([](const GemmMat& g) { return g.wg0; });
+    const int split = local / ntile;
+    const int n0 = (local - split * ntile) * BN, m0 = blockIdx.y * BM;
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
-    // super-blocks [gbeg, gend) of the K split (all of them when gridDim.z == 1); with P the sums go
-    // to partial plane blockIdx.z (rows of R floats) instead of Y
-    const int gbeg = blockIdx.z * gps, gend = gbeg + gps < G ? gbeg + gps : G;
-    float* const Yo = P ? P + (int64_t)blockIdx.z * pstride : Y;
+    // super-blocks [gbeg, gend) of the K split (all of them without one); with P the sums go to
+    // partial plane `split` (rows of R floats) instead of Y
+    const int gbeg = split * gps, gend = gbeg + gps < G ? gbeg + gps : G;
+    float* const Yo = P ? P + (int64_t)split * M * R : Y;
     const int64_t ldo = P ? (int64_t)R : ldy;
 
     // A operand of this lane for K step ks of super-block g: afrag[mt] + g * AG + ks * AK
@@ -516,41 +547,48 @@ static void gemm_split(int R, int C, int M, int& S, int& gps) {
 
 static size_t frag_bytes(int C, int M) { return (size_t)((M + GM_BMAX - 1) / GM_BMAX) * GM_BMAX * (size_t)C; }
 
-size_t gemm_q8k_workspace(int R, int C, int M) {
-    int S, gps;
-    gemm_split(R, C, M, S, gps);
-    const size_t f = (frag_bytes(C, M) + 255) / 256 * 256;
-    return S > 1 ? f + (size_t)S * M * R * sizeof(float) : f;
+// Workspace of a call over n matrices sharing the activations: the fragment copy (256-byte
+// aligned), then the partial planes of each matrix that splits K, back to back (multiples of 32
+// bytes: R is a multiple of 8).  For one matrix this is kq_gemm_q8k_workspace.
+size_t gemm_q8k_group_workspace(int n, const int* R, int C, int M) {
+    size_t total = (frag_bytes(C, M) + 255) / 256 * 256;
+    for (int i = 0; i < n; i++) {
+        int S, gps;
+        gemm_split(R[i], C, M, S, gps);
+        if (S > 1) total += (size_t)S * M * R[i] * sizeof(float);
+    }
+    return total;
 }
 
+size_t gemm_q8k_workspace(int R, int C, int M) { return gemm_q8k_group_workspace(1, &R, C, M); }
+
 template <int TYPE, int BN, int WN, int WM>
-static void launch_tile(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
-                        int64_t ldy, int S, int gps, float* part, hipStream_t s) {
+static void launch_tile(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, const uint8_t* xf, int M,
+                        const int* S, hipStream_t s) {
     constexpr int BM = 64 * WM;
     static_assert(BN == GM_TN && BM == GM_TM, "the split rule assumes these tiles");
-    dim3 grid((R + BN - 1) / BN, (M + BM - 1) / BM, S), block(64 * WN * WM);
-    const int64_t pstride = (int64_t)M * R;
+    dim3 grid(wgs, (M + BM - 1) / BM), block(64 * WN * WM);
     if (xf)
-        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy, gps,
-                           part, pstride);
+        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true>), grid, block, 0, s, gg, G, xq, xf, M);
     else
-        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false>), grid, block, 0, s, w, R, G, xq, xf, M, y, ldy, gps,
-                           part, pstride);
-    if (part) {
-        const int64_t n4 = (int64_t)M * (R / 4);
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, part, S, pstride, M,
-                           R, y, ldy);
+        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false>), grid, block, 0, s, gg, G, xq, xf, M);
+    for (int i = 0; i < gg.n; i++) {
+        const GemmMat& mt = gg.m[i];
+        if (!mt.part) continue;
+        const int64_t n4 = (int64_t)M * (mt.R / 4);
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, mt.part, S[i],
+                           (int64_t)M * mt.R, M, mt.R, mt.y, mt.ldy);
     }
 }
 
 template <int TYPE>
-static void launch_type(const uint8_t* w, int R, int G, const uint8_t* xq, const uint8_t* xf, int M, float* y,
-                        int64_t ldy, int S, int gps, float* part, hipStream_t s) {
+static void launch_type(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, const uint8_t* xf, int M,
+                        const int* S, hipStream_t s) {
     // 128 tokens x 64 weight rows per workgroup of 4 waves (80 KB of LDS, at most 256 VGPRs), so two
     // workgroups share a CU and each SIMD holds two waves: one wave's unpack and epilogue run under
     // the other's MFMAs.  (Measured against 128 x 128 tiles, one wave per SIMD, 4-8 waves per
     // workgroup: 289-317 against 331-379 us at M = 2048.)
-    launch_tile<TYPE, 64, 2, 2>(w, R, G, xq, xf, M, y, ldy, S, gps, part, s);
+    launch_tile<TYPE, 64, 2, 2>(gg, wgs, G, xq, xf, M, S, s);
 }
 
 // ------------------------------------------------------------------ the no-allocation form
@@ -588,20 +626,60 @@ int gemm_static_scratch(uint8_t** out, const char* fn) {
     return KQ_OK;
 }
 
-void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
-                     uint8_t* ws, hipStream_t s) {
+void launch_gemm_q8k_group(int n, const uint8_t* const* w, const int* R, int C, const int* type, const uint8_t* xq,
+                           int M, float* const* y, const int64_t* ldy, uint8_t* ws, hipStream_t s) {
     const int G = C / QK;
-    int S = 1, gps = G;
-    float* part = nullptr;
-    if (ws) {
+    if (ws) {   // one fragment copy serves every matrix of the call
         dim3 fgrid((M + GM_BMAX - 1) / GM_BMAX * (GM_BMAX / 32), G);
         hipLaunchKernelGGL(k_q8k_frag, fgrid, dim3(256), 0, s, xq, M, G, ws);
-        gemm_split(R, C, M, S, gps);
-        if (S > 1) part = reinterpret_cast<float*>(ws + (frag_bytes(C, M) + 255) / 256 * 256);
-        else gps = G;
     }
-    if (type == TYPE_Q4_K) launch_type<TYPE_Q4_K>(w, R, G, xq, ws, M, y, ldy, S, gps, part, s);
-    else launch_type<TYPE_Q6_K>(w, R, G, xq, ws, M, y, ldy, S, gps, part, s);
+    // each matrix's split and partial planes, as a call of its own would take them
+    int S[3], gps[3];
+    float* part[3];
+    size_t off = (frag_bytes(C, M) + 255) / 256 * 256;
+    for (int i = 0; i < n; i++) {
+        S[i] = 1;
+        gps[i] = G;
+        part[i] = nullptr;
+        if (ws) {
+            gemm_split(R[i], C, M, S[i], gps[i]);
+            if (S[i] > 1) {
+                part[i] = reinterpret_cast<float*>(ws + off);
+                off += (size_t)S[i] * M * R[i] * sizeof(float);
+            } else {
+                gps[i] = G;
+            }
+        }
+    }
+    // one launch per weight type, the matrices of that type in call order
+    for (int ty : {TYPE_Q4_K, TYPE_Q6_K}) {
+        GemmGroup gg{};
+        int Sg[3];
+        int wgs = 0;
+        for (int i = 0; i < n; i++) {
+            if (type[i] != ty) continue;
+            GemmMat& mt = gg.m[gg.n];
+            mt.w = w[i];
+            mt.y = y[i];
+            mt.part = part[i];
+            mt.ldy = ldy[i];
+            mt.R = R[i];
+            mt.ntile = (R[i] + GM_TN - 1) / GM_TN;
+            mt.gps = gps[i];
+            mt.wg0 = wgs;
+            Sg[gg.n] = S[i];
+            wgs += mt.ntile * S[i];
+            gg.n++;
+        }
+        if (!gg.n) continue;
+        if (ty == TYPE_Q4_K) launch_type<TYPE_Q4_K>(gg, wgs, G, xq, ws, M, Sg, s);
+        else launch_type<TYPE_Q6_K>(gg, wgs, G, xq, ws, M, Sg, s);
+    }
+}
+
+void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
+                     uint8_t* ws, hipStream_t s) {
+    launch_gemm_q8k_group(1, &w, &R, C, &type, xq, M, &y, &ldy, ws, s);
 }
 
 }  // namespace kq

@@ -44,6 +44,11 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
 size_t gemm_q8k_workspace(int R, int C, int M);
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,
                      uint8_t* ws, hipStream_t s);
+// The same over n (1..3) matrices sharing xq: one fragment copy, one GEMM launch per weight type;
+// each matrix's results equal those of its own launch_gemm_q8k call bit for bit.
+size_t gemm_q8k_group_workspace(int n, const int* R, int C, int M);
+void launch_gemm_q8k_group(int n, const uint8_t* const* w, const int* R, int C, const int* type, const uint8_t* xq,
+                           int M, float* const* y, const int64_t* ldy, uint8_t* ws, hipStream_t s);
 // Device address of the static GEMM workspace on the current device (KQ_GEMM_STATIC_SCRATCH_BYTES),
 // looked up on the first call per device; fails with KQ_ERR_HIP when the lookup fails.
 int gemm_static_scratch(uint8_t** out, const char* fn);

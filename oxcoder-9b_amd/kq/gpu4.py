@@ -103,12 +103,14 @@ class Engine:
         dev = self.device
         # Q8_K workspace (the reference's reused xp scratch, gpu4.py:70-79)
         self.xq = torch.empty(self.max_rows * (cols // QK) * Q8K_BYTES, dtype=torch.uint8, device=dev)
-        # prefill GEMM workspace: the most any chunk (1..chunk rows) of any matrix needs
+        # prefill GEMM workspace: the most any chunk (1..chunk rows) of up to three matrices sharing
+        # an input needs (three of the same shape bound every mix)
         need = 0
         if self.chunk:
             for R, C in shapes:
                 if C <= cols:
-                    need = max(need, max(ops.gemm_workspace_bytes(R, C, m) for m in range(1, self.chunk + 1)))
+                    need = max(need, max(ops.gemm_multi_workspace_bytes([R, R, R], C, m)
+                                         for m in range(1, self.chunk + 1)))
         self.gemm_ws = torch.empty(need + 256, dtype=torch.uint8, device=dev) if need else None
         self.argmax_ws = ops.argmax_workspace(dev)
         self.argmax_out = torch.empty(1, dtype=torch.int32, device=dev)
@@ -247,9 +249,10 @@ class Engine:
     def gemm(self, names, X, outs):
         """Prefill GEMM over any number M of rows of X [M][C], in chunks of ``chunk`` tokens as the
         reference's chunked prefill feeds them (chunk.py:165-177,378): each chunk is quantized once
-        into the engine's Q8_K workspace, then every named matrix runs the GEMM on it with the
-        engine's GEMM workspace (kq_gemm_q8k_ws).  Chunk results equal one kq_gemm_q8k_ws call on
-        that chunk bit for bit.  Allocates nothing."""
+        into the engine's Q8_K workspace, then the named matrices run the GEMM on it three at a time
+        (kq_gemm_q8k_multi_ws: one fragment copy and one launch per weight type for the three) with
+        the engine's GEMM workspace.  Chunk results equal one kq_gemm_q8k_ws call per matrix on that
+        chunk bit for bit.  Allocates nothing."""
         M, C = X.shape
         if not self.chunk:
             raise ValueError("chunked prefill is off (chunk 0): use feed_rows or gemv_batch")
@@ -261,10 +264,10 @@ class Engine:
         for m0 in range(0, M, self.chunk):
             mc = min(self.chunk, M - m0)
             xq = self._quantize(X[m0:m0 + mc], C)
-            for (w, R, C_, ty), y in zip(mats, outs):
-                ldy = y.stride(0) if y.dim() == 2 else R     # a flat output holds rows of R
-                yv = y[m0:m0 + mc] if y.dim() == 2 else y[m0 * R:]
-                ops.gemm_q8k(w, R, C_, ty, xq, mc, yv, ldy, ws=self.gemm_ws)
+            # a flat output holds rows of R
+            views = [y[m0:m0 + mc] if y.dim() == 2 else y[m0 * R:] for (_, R, _, _), y in zip(mats, outs)]
+            for i in range(0, len(mats), 3):
+                ops.gemm_q8k_multi(mats[i:i + 3], xq, mc, views[i:i + 3], self.gemm_ws)
         return 1
 
     def embed(self, tok, out=None, name="token_embd.weight"):

@@ -283,6 +283,34 @@ def test_gemm_q8k_split_k(dev, orc, ty, R, C, M, S):
     np.testing.assert_array_equal(host(y2)[:, :R], got[:, :R])
 
 
+@pytest.mark.parametrize("C,M", [(4096, 256), (4096, 300), (12288, 130), (2048, 2048)])
+def test_gemm_q8k_multi_matches_single(dev, orc, C, M):
+    """A q/k/v-style group (two Q4_K matrices, one Q6_K) in one kq_gemm_q8k_multi_ws call: one
+    fragment copy, one launch per type, each matrix keeping the K split of its own call, so every
+    output equals kq_gemm_q8k_ws on that matrix alone bit for bit (splitting and unsplit shapes
+    alike), columns past R untouched; the small matrices also against the oracle."""
+    print("gemm multi", C, M, flush=True)
+    shapes = [(4096, 12), (1024, 12), (1024, 14)]
+    mats_h = [(synth(R, C, ty, 90 + i), R, C, ty) for i, (R, ty) in enumerate(shapes)]
+    mats = [(dev_t(W, dev), R, C_, ty) for (W, R, C_, ty) in mats_h]
+    xq = orc.quantize_q8k(kqq.synthetic_activations(M, C, seed=M + 11))
+    xqd = dev_t(xq, dev)
+    need = ops.gemm_multi_workspace_bytes([R for R, _ in shapes], C, M)
+    frag = -(-M // 256) * 256 * C                   # fragment copy (a multiple of 256 bytes)
+    assert need == frag + sum(ops.gemm_workspace_bytes(R, C, M) - frag for R, _ in shapes)
+    ws = torch.full((need + 256,), 0x55, dtype=torch.uint8, device=dev)
+    ys = [torch.full((M, R + 4), -7.0, device=dev) for (_, R, _, _) in mats]
+    ops.gemm_q8k_multi(mats, xqd, M, ys, ws)
+    for (w, R, C_, ty), y, (W, _, _, _) in zip(mats, ys, mats_h):
+        ref = torch.empty((M, R), device=dev)
+        ops.gemm_q8k(w, R, C_, ty, xqd, M, ref, ws=ops.gemm_workspace(R, C_, M, dev))
+        got = host(y)
+        np.testing.assert_array_equal(got[:, :R], host(ref))
+        assert np.all(got[:, R:] == -7.0)
+        if R <= 1024:
+            assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C_, ty, xq, M))
+
+
 @pytest.mark.parametrize("ty", [12, 14])
 def test_gemm_q8k_reference_inputs(dev, orc, ty):
     """The reference unit test's random block bytes (any scale/min bit pattern) through the GEMM."""

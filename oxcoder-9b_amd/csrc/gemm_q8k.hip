@@ -496,13 +496,33 @@ k_q8k_frag(const uint8_t* __restrict__ XQ, int M, int G, uint8_t* __restrict__ X
 }
 
 // Partial planes y_s[m][r] of the K split, added in order s = 0 .. S-1: y = ((y_0 + y_1) + y_2) + ...
-// One thread per 4 consecutive outputs of a row.
+// One launch for every split matrix of a call: workgroups [blk0[j], blk0[j+1]) serve matrix j, one
+// thread per 4 consecutive outputs of a row.
+struct ReduceMat {
+    const float* part;
+    float* y;
+    int64_t ldy;
+    int R, S, blk0;
+};
+struct ReduceGroup {
+    ReduceMat m[3];
+    int n;
+};
+
 __global__ void __launch_bounds__(256)
-k_gemm_reduce(const float* __restrict__ P, int S, int64_t pstride, int M, int R, float* __restrict__ Y,
-              int64_t ldy) {
+k_gemm_reduce(ReduceGroup rg, int M) {
+    const int bx = blockIdx.x;
+    const int j = rg.n > 1 && bx >= rg.m[1].blk0 ? (rg.n > 2 && bx >= rg.m[2].blk0 ? 2 : 1) : 0;
+    auto field = [&](auto get) { return j == 0 ? get(rg.m[0]) : j == 1 ? get(rg.m[1]) : get(rg.m[2]); };
+    const float* const P = field([](const ReduceMat& g) { return g.part; });
+    float* const Y = field([](const ReduceMat& g) { return g.y; });
+    const int64_t ldy = field([](const ReduceMat& g) { return g.ldy; });
+    const int R = field([](const ReduceMat& g) { return g.R; });
+    const int S = field([](const ReduceMat& g) { return g.S; });
     const int r4 = R >> 2;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = (int64_t)(bx - field([](const ReduceMat& g) { return g.blk0; })) * 256 + threadIdx.x;
     if (i >= (int64_t)M * r4) return;
+    const int64_t pstride = (int64_t)M * R;
     const int m = (int)(i / r4), r = (int)(i - (int64_t)m * r4) * 4;
     const float* p = P + (int64_t)m * R + r;
     f32x4 a = *reinterpret_cast<const f32x4*>(p);
@@ -572,13 +592,22 @@ static void launch_tile(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, 
         hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true>), grid, block, 0, s, gg, G, xq, xf, M);
     else
         hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false>), grid, block, 0, s, gg, G, xq, xf, M);
+    // one reduce launch for the matrices that split K
+    ReduceGroup rg{};
+    int blks = 0;
     for (int i = 0; i < gg.n; i++) {
         const GemmMat& mt = gg.m[i];
         if (!mt.part) continue;
-        const int64_t n4 = (int64_t)M * (mt.R / 4);
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, mt.part, S[i],
-                           (int64_t)M * mt.R, M, mt.R, mt.y, mt.ldy);
+        ReduceMat& rm = rg.m[rg.n++];
+        rm.part = mt.part;
+        rm.y = mt.y;
+        rm.ldy = mt.ldy;
+        rm.R = mt.R;
+        rm.S = S[i];
+        rm.blk0 = blks;
+        blks += (int)(((int64_t)M * (mt.R / 4) + 255) / 256);
     }
+    if (rg.n) hipLaunchKernelGGL(k_gemm_reduce, dim3(blks), dim3(256), 0, s, rg, M);
 }
 
 template <int TYPE>

@@ -669,15 +669,17 @@ def decode_stream_extra(torch, rn, dev):
 
 def prefill_chunk_extra(torch, rn, dev, layers, M=256):
     """One prefill chunk of M tokens (the Engine's KINDI_CHUNK) through a decode layer's 7 matrices, as
-    Engine.gemm runs it: each of the 4 inputs quantized once (M rows), then the matrices sharing it
-    in one kq_gemm_q8k_multi_ws call (one fragment copy, one GEMM launch); beside it the same chunk
-    with one kq_gemm_q8k_ws call per matrix.  The resident layer copies rotate."""
+    Engine.gemm runs it: for each of the 4 fp32 inputs one kq_gemm_f32_multi call for the matrices
+    sharing it (one launch quantizes the chunk and writes the GEMM's fragment copy, one GEMM launch);
+    beside it the same chunk with kq_q8k_quantize and one kq_gemm_q8k_ws call per matrix.  The
+    resident layer copies rotate."""
     from kq import ops, quantize as kqq
     xs = [torch.from_numpy(kqq.synthetic_activations(M, c, seed=10 + s)).to(dev) for s, c in enumerate(INPUT_COLS)]
     xqs = [torch.empty(M * (c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
     ys = {name: torch.empty((M, R), device=dev) for name, R, _, _, _ in LAYER}
     groups = [[(n, R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == slot] for slot in range(len(INPUT_COLS))]
-    need = max(ops.gemm_multi_workspace_bytes([R for _, R, _, _ in g], g[0][2], M) for g in groups)
+    need = max(ops.gemm_f32_multi_workspace_bytes([R for _, R, _, _ in g], g[0][2], M) for g in groups)
+    need = max(need, max(ops.gemm_workspace_bytes(R, C_, M) for _, R, C_, _, _ in LAYER))
     ws = torch.empty(need + 256, dtype=torch.uint8, device=dev)
     wsa = ws[(-ws.data_ptr()) % 256:]
     copies = min(len(layers), 8)
@@ -687,14 +689,14 @@ def prefill_chunk_extra(torch, rn, dev, layers, M=256):
             s = rn.stream()
             for lay in layers[:copies]:
                 for slot, c in enumerate(INPUT_COLS):
+                    if grouped:
+                        ops.gemm_f32_multi([(lay[n], R, C2, ty) for n, R, C2, ty in groups[slot]], xs[slot],
+                                           [ys[n] for n, *_ in groups[slot]], ws)
+                        continue
                     rn.check(rn.lib.kq_q8k_quantize(C.c_void_p(xs[slot].data_ptr()), c, c, M,
                                                     C.c_void_p(xqs[slot].data_ptr()), s))
-                    if grouped:
-                        ops.gemm_q8k_multi([(lay[n], R, C2, ty) for n, R, C2, ty in groups[slot]], xqs[slot], M,
-                                           [ys[n] for n, *_ in groups[slot]], ws)
-                    else:
-                        for n, R, C2, ty in groups[slot]:
-                            rn.gemm(lay[n], R, C2, ty, xqs[slot], M, ys[n], wsa, s)
+                    for n, R, C2, ty in groups[slot]:
+                        rn.gemm(lay[n], R, C2, ty, xqs[slot], M, ys[n], wsa, s)
 
         g = capture(torch, fn)
         warm = 0.0

@@ -181,6 +181,18 @@ int kq_gemm_q8k_multi_ws(int n, const void* const* w, const int* R, int C, const
                          float* const* y, const int64_t* ldy, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * The same from fp32 activations: x holds M rows of C floats (row stride ldx, 4-byte aligned), which
+ * one launch quantizes to Q8_K (as kq_q8k_quantize, same bytes) into the workspace, writing the GEMM's
+ * fragment copy at the same time; then the grouped GEMM.  This is the chunked prefill's step: each
+ * chunk's hidden states quantized once for the projections that share them (chunk.py:165-177).  ws
+ * (256-byte aligned) holds kq_gemm_f32_multi_workspace(n, R, C, M) bytes; every y[i] equals
+ * kq_q8k_quantize followed by kq_gemm_q8k_ws on that matrix, bit for bit.
+ */
+size_t kq_gemm_f32_multi_workspace(int n, const int* R, int C, int M);
+int kq_gemm_f32_multi(int n, const void* const* w, const int* R, int C, const int* type, const float* x, int64_t ldx,
+                      int M, float* const* y, const int64_t* ldy, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * kq_gemm_q8k_ws without a caller workspace and without any allocation: the workspace is the
  * library's static device array of KQ_GEMM_STATIC_SCRATCH_BYTES (one per device, held until the
  * process ends; a 256-token prefill chunk of every 9B-model matrix fits).  No counterpart in the

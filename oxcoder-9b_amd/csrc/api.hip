@@ -231,15 +231,20 @@ int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const in
     return check_launch(fn);
 }
 
-static int check_gemm(const void* w, int R, int C, int type, const void* xq, int M, const float* y, int64_t ldy,
-                      const char* fn) {
+// A GEMM's matrix, M and output (the activations are checked by the caller).
+static int check_gemm_out(const void* w, int R, int C, int type, int M, const float* y, int64_t ldy, const char* fn) {
     KQ_TRY(check_matrix(w, R, C, type, fn));
     if (M < 1) return fail(KQ_ERR_ARG, "%s: M=%d must be positive", fn, M);
     if (M > 1 && ldy < R) return fail(KQ_ERR_ARG, "%s: ldy=%lld is smaller than R=%d", fn, (long long)ldy, R);
-    KQ_TRY(check_ptr(xq, 4, "xq", fn));
     KQ_TRY(check_ptr(y, 4, "y", fn));
     if ((int64_t)M * (C / 256) > 0x7fffffffLL) return fail(KQ_ERR_ARG, "%s: M*C/256 too large", fn);
     return KQ_OK;
+}
+
+static int check_gemm(const void* w, int R, int C, int type, const void* xq, int M, const float* y, int64_t ldy,
+                      const char* fn) {
+    KQ_TRY(check_gemm_out(w, R, C, type, M, y, ldy, fn));
+    return check_ptr(xq, 4, "xq", fn);
 }
 
 int kq_gemm_q8k(const void* w, int R, int C, int type, const void* xq, int M, float* y,
@@ -288,6 +293,28 @@ int kq_gemm_q8k_multi_ws(int n, const void* const* w, const int* R, int C, const
     for (int i = 0; i < n; i++) wb[i] = static_cast<const uint8_t*>(w[i]);
     launch_gemm_q8k_group(n, wb, R, C, type, static_cast<const uint8_t*>(xq), M, y, ldy, static_cast<uint8_t*>(ws),
                           as_stream(stream));
+    return check_launch(fn);
+}
+
+size_t kq_gemm_f32_multi_workspace(int n, const int* R, int C, int M) {
+    if (!kq_gemm_q8k_multi_workspace(n, R, C, M)) return 0;
+    return gemm_f32_group_workspace(n, R, C, M);
+}
+
+int kq_gemm_f32_multi(int n, const void* const* w, const int* R, int C, const int* type, const float* x, int64_t ldx,
+                      int M, float* const* y, const int64_t* ldy, void* ws, size_t ws_bytes, void* stream) {
+    static const char* fn = "kq_gemm_f32_multi";
+    if (n < 1 || n > 3) return fail(KQ_ERR_ARG, "%s: n=%d must be 1..3", fn, n);
+    if (!w || !R || !type || !y || !ldy) return fail(KQ_ERR_ARG, "%s: NULL array argument", fn);
+    KQ_TRY(check_ptr(x, 4, "x", fn));
+    if (M > 1 && ldx < C) return fail(KQ_ERR_ARG, "%s: ldx=%lld is smaller than C=%d", fn, (long long)ldx, C);
+    for (int i = 0; i < n; i++) KQ_TRY(check_gemm_out(w[i], R[i], C, type[i], M, y[i], ldy[i], fn));
+    KQ_TRY(check_ptr(ws, 256, "ws", fn));
+    const size_t need = gemm_f32_group_workspace(n, R, C, M);
+    if (ws_bytes < need) return fail(KQ_ERR_ARG, "%s: workspace of %zu bytes, %zu needed", fn, ws_bytes, need);
+    const uint8_t* wb[3];
+    for (int i = 0; i < n; i++) wb[i] = static_cast<const uint8_t*>(w[i]);
+    launch_gemm_f32_group(n, wb, R, C, type, x, ldx, M, y, ldy, static_cast<uint8_t*>(ws), as_stream(stream));
     return check_launch(fn);
 }
 

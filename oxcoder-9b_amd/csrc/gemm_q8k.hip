@@ -656,9 +656,9 @@ int gemm_static_scratch(uint8_t** out, const char* fn) {
 }
 
 void launch_gemm_q8k_group(int n, const uint8_t* const* w, const int* R, int C, const int* type, const uint8_t* xq,
-                           int M, float* const* y, const int64_t* ldy, uint8_t* ws, hipStream_t s) {
+                           int M, float* const* y, const int64_t* ldy, uint8_t* ws, hipStream_t s, bool frag_ready) {
     const int G = C / QK;
-    if (ws) {   // one fragment copy serves every matrix of the call
+    if (ws && !frag_ready) {   // one fragment copy serves every matrix of the call
         dim3 fgrid((M + GM_BMAX - 1) / GM_BMAX * (GM_BMAX / 32), G);
         hipLaunchKernelGGL(k_q8k_frag, fgrid, dim3(256), 0, s, xq, M, G, ws);
     }
@@ -704,6 +704,20 @@ void launch_gemm_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
         if (ty == TYPE_Q4_K) launch_type<TYPE_Q4_K>(gg, wgs, G, xq, ws, M, Sg, s);
         else launch_type<TYPE_Q6_K>(gg, wgs, G, xq, ws, M, Sg, s);
     }
+}
+
+static size_t q8k_rows_bytes(int C, int M) { return ((size_t)M * (C / QK) * Q8K_BYTES + 255) / 256 * 256; }
+
+size_t gemm_f32_group_workspace(int n, const int* R, int C, int M) {
+    return q8k_rows_bytes(C, M) + gemm_q8k_group_workspace(n, R, C, M);
+}
+
+void launch_gemm_f32_group(int n, const uint8_t* const* w, const int* R, int C, const int* type, const float* x,
+                           int64_t ldx, int M, float* const* y, const int64_t* ldy, uint8_t* ws, hipStream_t s) {
+    uint8_t* xq = ws;
+    uint8_t* gws = ws + q8k_rows_bytes(C, M);
+    launch_q8k_quantize_frag(x, ldx, C, M, (M + GM_BMAX - 1) / GM_BMAX * GM_BMAX, xq, gws, s);
+    launch_gemm_q8k_group(n, w, R, C, type, xq, M, y, ldy, gws, s, true);
 }
 
 void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq, int M, float* y, int64_t ldy,

@@ -26,6 +26,10 @@ inline int block_bytes(int type) { return type == KQ_TYPE_Q4_K ? 144 : 210; }
 
 // Launchers implemented by the kernel translation units.  Arguments are already validated.
 void launch_q8k_quantize(const float* x, int64_t ldx, int C, int N, uint8_t* xq, hipStream_t s);
+// The same for M rows, also writing the prefill GEMM's fragment copy xf (Mpad >= M rows, the rows past
+// M zero).
+void launch_q8k_quantize_frag(const float* x, int64_t ldx, int C, int M, int Mpad, uint8_t* xq, uint8_t* xf,
+                              hipStream_t s);
 // Fused producers of Q8_K activations (RMSNorm with optional residual add; SwiGLU).
 void launch_rms_q8k(float* h, const float* res, int add, const float* w, int D, int N, int64_t ld, float* xn,
                     uint8_t* xq, hipStream_t s);
@@ -48,7 +52,14 @@ void launch_gemm_q8k(const uint8_t* w, int R, int C, int type, const uint8_t* xq
 // each matrix's results equal those of its own launch_gemm_q8k call bit for bit.
 size_t gemm_q8k_group_workspace(int n, const int* R, int C, int M);
 void launch_gemm_q8k_group(int n, const uint8_t* const* w, const int* R, int C, const int* type, const uint8_t* xq,
-                           int M, float* const* y, const int64_t* ldy, uint8_t* ws, hipStream_t s);
+                           int M, float* const* y, const int64_t* ldy, uint8_t* ws, hipStream_t s,
+                           bool frag_ready = false);
+// From fp32 activations: x (M rows, stride ldx) quantized once into the workspace, as Q8_K rows and
+// the fragment copy in one launch, then the grouped GEMM.  Workspace: the Q8_K rows (256-byte
+// aligned), then gemm_q8k_group_workspace.
+size_t gemm_f32_group_workspace(int n, const int* R, int C, int M);
+void launch_gemm_f32_group(int n, const uint8_t* const* w, const int* R, int C, const int* type, const float* x,
+                           int64_t ldx, int M, float* const* y, const int64_t* ldy, uint8_t* ws, hipStream_t s);
 // Device address of the static GEMM workspace on the current device (KQ_GEMM_STATIC_SCRATCH_BYTES),
 // looked up on the first call per device; fails with KQ_ERR_HIP when the lookup fails.
 int gemm_static_scratch(uint8_t** out, const char* fn);

@@ -11,8 +11,9 @@
 namespace kq {
 
 // e: this lane's values 4*lane .. 4*lane+3 of the block; ob: the block's 292 output bytes.
-// Every lane of the wave must call it (cross-lane reductions).
-__device__ __forceinline__ void q8k_block_store(const float (&e)[4], int lane, uint8_t* __restrict__ ob) {
+// Every lane of the wave must call it (cross-lane reductions).  Returns the lane's four quants
+// (qs bytes 4*lane .. 4*lane+3, as stored).
+__device__ __forceinline__ uint32_t q8k_block_store(const float (&e)[4], int lane, uint8_t* __restrict__ ob) {
     // max |x| over the block: butterfly max (exact, order-free); NaN never wins (v_max returns
     // the other operand), matching the strict "ax > amax" scan of the reference definition.
     float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(e[0]), __builtin_fabsf(e[1])),
@@ -60,6 +61,7 @@ __device__ __forceinline__ void q8k_block_store(const float (&e)[4], int lane, u
         const uint32_t pair = ((uint32_t)s4 & 0xffffu) | ((uint32_t)s_next << 16);
         *reinterpret_cast<uint32_t*>(ob + 260 + 4 * (lane >> 3)) = pair;
     }
+    return packed;
 }
 
 }  // namespace kq

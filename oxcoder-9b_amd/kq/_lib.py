@@ -33,6 +33,9 @@ KQ_SYMBOLS = {
     "kq_gemm_q8k_multi_workspace": (C.c_size_t, [_i, C.POINTER(_i), _i, _i]),
     "kq_gemm_q8k_multi_ws": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, _i, C.POINTER(_vp),
                                   C.POINTER(_i64), _vp, C.c_size_t, _vp]),
+    "kq_gemm_f32_multi_workspace": (C.c_size_t, [_i, C.POINTER(_i), _i, _i]),
+    "kq_gemm_f32_multi": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, _i64, _i, C.POINTER(_vp),
+                               C.POINTER(_i64), _vp, C.c_size_t, _vp]),
     "kq_gemm_q8k_static": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),
     "kq_subblock_sums": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _vp]),
     "kq_dequant_rows": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _i64, _vp]),

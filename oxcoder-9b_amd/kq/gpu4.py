@@ -109,7 +109,7 @@ class Engine:
         if self.chunk:
             for R, C in shapes:
                 if C <= cols:
-                    need = max(need, max(ops.gemm_multi_workspace_bytes([R, R, R], C, m)
+                    need = max(need, max(ops.gemm_f32_multi_workspace_bytes([R, R, R], C, m)
                                          for m in range(1, self.chunk + 1)))
         self.gemm_ws = torch.empty(need + 256, dtype=torch.uint8, device=dev) if need else None
         self.argmax_ws = ops.argmax_workspace(dev)
@@ -172,7 +172,7 @@ class Engine:
         """h += residual (when given, in place), then RMSNorm(h) * w written as Q8_K into the engine
         workspace (and to xn when given).  Returns (xn, xq) for gemv_q8.  xq is a view of the engine's
         one Q8_K workspace (like the reference's reused xp scratch, gpu4.py:70-79): the next call that
-        quantizes (gemv in "q8k" mode, gemv_batch, gemm, feed_rows, head, rmsfold_q8k, swiglu_q8k)
+        quantizes (gemv in "q8k" mode, gemv_batch, feed_rows, head, rmsfold_q8k, swiglu_q8k)
         overwrites it."""
         N = 1 if h.dim() == 1 else h.shape[0]
         D = h.shape[-1]
@@ -248,11 +248,11 @@ class Engine:
 
     def gemm(self, names, X, outs):
         """Prefill GEMM over any number M of rows of X [M][C], in chunks of ``chunk`` tokens as the
-        reference's chunked prefill feeds them (chunk.py:165-177,378): each chunk is quantized once
-        into the engine's Q8_K workspace, then the named matrices run the GEMM on it three at a time
-        (kq_gemm_q8k_multi_ws: one fragment copy and one launch per weight type for the three) with
-        the engine's GEMM workspace.  Chunk results equal one kq_gemm_q8k_ws call per matrix on that
-        chunk bit for bit.  Allocates nothing."""
+        reference's chunked prefill feeds them (chunk.py:165-177,378): the named matrices go three at
+        a time through kq_gemm_f32_multi, which quantizes the chunk once into the engine's GEMM
+        workspace (Q8_K rows and the GEMM's fragment copy in one launch) and runs one GEMM launch per
+        weight type.  Chunk results equal kq_q8k_quantize then one kq_gemm_q8k_ws call per matrix on
+        that chunk, bit for bit.  Allocates nothing."""
         M, C = X.shape
         if not self.chunk:
             raise ValueError("chunked prefill is off (chunk 0): use feed_rows or gemv_batch")
@@ -261,13 +261,14 @@ class Engine:
             if C_ != C:
                 raise ValueError("column count mismatch")
             self._check_out(y, R, M)
+        if C > self.max_cols:
+            raise ValueError("input of %d columns exceeds the engine workspace (%d)" % (C, self.max_cols))
         for m0 in range(0, M, self.chunk):
             mc = min(self.chunk, M - m0)
-            xq = self._quantize(X[m0:m0 + mc], C)
             # a flat output holds rows of R
             views = [y[m0:m0 + mc] if y.dim() == 2 else y[m0 * R:] for (_, R, _, _), y in zip(mats, outs)]
             for i in range(0, len(mats), 3):
-                ops.gemm_q8k_multi(mats[i:i + 3], xq, mc, views[i:i + 3], self.gemm_ws)
+                ops.gemm_f32_multi(mats[i:i + 3], X[m0:m0 + mc], views[i:i + 3], self.gemm_ws)
         return 1
 
     def embed(self, tok, out=None, name="token_embd.weight"):

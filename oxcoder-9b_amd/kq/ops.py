@@ -282,6 +282,43 @@ def gemm_q8k_multi(mats, xq, M, ys, ws):
     return ys
 
 
+def gemm_f32_multi_workspace_bytes(Rs, C_, M):
+    """Device bytes of workspace gemm_f32_multi needs (kq_gemm_f32_multi_workspace)."""
+    n = len(Rs)
+    return int(_lib.kq().kq_gemm_f32_multi_workspace(n, (C.c_int * n)(*Rs), C_, M))
+
+
+def gemm_f32_multi(mats, X, ys, ws):
+    """Prefill GEMM of up to 3 matrices [(w, R, C, type)] on fp32 activations X [M][C] (unit stride
+    along C): one launch quantizes X into the workspace (Q8_K rows and the fragment copy), then one
+    GEMM launch per type (kq_gemm_f32_multi).  ys[i] is [M][ld_i] or flat (rows of R_i); ws a device
+    uint8 tensor of at least gemm_f32_multi_workspace_bytes + 256 bytes."""
+    n = len(mats)
+    if not 1 <= n <= 3 or len(ys) != n:
+        raise ValueError("1..3 matrices with one output each")
+    M, C_ = X.shape
+    if any(m[2] != C_ for m in mats):
+        raise ValueError("matrices sharing an input must have its column count")
+    if X.stride(1) != 1:
+        raise ValueError("X needs unit stride along its rows")
+    W = (C.c_void_p * n)(*[_weights(w, R, C_, ty).value for (w, R, _, ty) in mats])
+    Rs = (C.c_int * n)(*[m[1] for m in mats])
+    Ts = (C.c_int * n)(*[m[3] for m in mats])
+    lds = []
+    for (w, R, _, ty), y in zip(mats, ys):
+        ld = y.stride(0) if y.dim() == 2 else R
+        if y.numel() < (M - 1) * ld + R:
+            raise ValueError("output too small")
+        lds.append(ld)
+    Y = (C.c_void_p * n)(*[_dev(y, "y", torch.float32).value for y in ys])
+    L = (C.c_int64 * n)(*lds)
+    _dev(ws, "ws", torch.uint8)
+    pws, nws = _aligned(ws, gemm_f32_multi_workspace_bytes([m[1] for m in mats], C_, M))
+    _lib.check(_lib.kq().kq_gemm_f32_multi(n, W, Rs, C_, Ts, _dev(X, "X", torch.float32), X.stride(0), M, Y, L,
+                                           pws, nws, _stream(mats[0][0].device)))
+    return ys
+
+
 def subblock_sums(w, R, C_, ty, xq, N):
     """Exact int32 sub-block sums [N][R][G][8 or 16] (kq_subblock_sums)."""
     pw = _weights(w, R, C_, ty)

@@ -311,6 +311,43 @@ def test_gemm_q8k_multi_matches_single(dev, orc, C, M):
             assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C_, ty, xq, M))
 
 
+@pytest.mark.parametrize("C,M,ldx", [(4096, 256, 4096), (4096, 300, 4352), (12288, 130, 12288), (2048, 257, 2048)])
+def test_gemm_f32_multi_matches_quantize_then_gemm(dev, orc, C, M, ldx):
+    """kq_gemm_f32_multi (one launch quantizing the fp32 rows into the workspace and writing the GEMM's
+    fragment copy, then the grouped GEMM) equals kq_q8k_quantize followed by kq_gemm_q8k_ws on each
+    matrix bit for bit, with strided input rows and a ragged last token tile (its pad rows zero)."""
+    print("gemm f32 multi", C, M, ldx, flush=True)
+    shapes = [(4096, 12), (1024, 14), (1024, 12)]
+    mats_h = [(synth(R, C, ty, 70 + i), R, C, ty) for i, (R, ty) in enumerate(shapes)]
+    mats = [(dev_t(W, dev), R, C_, ty) for (W, R, C_, ty) in mats_h]
+    Xw = np.zeros((M, ldx), np.float32)
+    Xw[:, :C] = kqq.synthetic_activations(M, C, seed=M + 23)
+    X = dev_t(Xw, dev)[:, :C]
+    need = ops.gemm_f32_multi_workspace_bytes([R for R, _ in shapes], C, M)
+    ws = torch.full((need + 256,), 0x33, dtype=torch.uint8, device=dev)
+    ys = [torch.full((M, R + 4), -7.0, device=dev) for (_, R, _, _) in mats]
+    ops.gemm_f32_multi(mats, X, ys, ws)
+    # the workspace: the Q8_K rows (256-byte aligned), then the fragment copy of M rounded up to 256 rows
+    G = C // 256
+    want = orc.quantize_q8k(Xw[:, :C]).reshape(M, G, 292)
+    wsh = host(ws)[(-ws.data_ptr()) % 256:]
+    nq = -(-M * G * 292 // 256) * 256
+    np.testing.assert_array_equal(wsh[:M * G * 292].reshape(M, G, 292), want)
+    Mp = -(-M // 256) * 256
+    qs = np.zeros((Mp, G, 256), np.uint8)
+    qs[:M] = want[:, :, 4:260]
+    # frag[m/32][g][ks][lane][16] = qs[32 (m/32) + lane % 32][g][32 ks + 16 (lane / 32) .. +16]
+    frag = qs.reshape(Mp // 32, 32, G, 8, 2, 16).transpose(0, 2, 3, 4, 1, 5).reshape(-1)
+    np.testing.assert_array_equal(wsh[nq:nq + Mp * C], frag)
+    xq = ops.q8k_quantize(X)
+    for (w, R, C_, ty), y in zip(mats, ys):
+        ref = torch.empty((M, R), device=dev)
+        ops.gemm_q8k(w, R, C_, ty, xq, M, ref, ws=ops.gemm_workspace(R, C_, M, dev))
+        got = host(y)
+        np.testing.assert_array_equal(got[:, :R], host(ref))
+        assert np.all(got[:, R:] == -7.0)
+
+
 @pytest.mark.parametrize("ty", [12, 14])
 def test_gemm_q8k_reference_inputs(dev, orc, ty):
     """The reference unit test's random block bytes (any scale/min bit pattern) through the GEMM."""

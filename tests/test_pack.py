@@ -188,8 +188,11 @@ def test_engine_over_a_pack_sizes_its_workspace_from_the_index(tiny_pack):
         eng = Engine(w, mode="q8k")
         assert eng.max_cols == 512
         assert eng.chunk == 256 and eng.xq.numel() == 256 * (512 // 256) * 292
-        # the GEMM workspace covers any chunk of 1..256 rows of every quantized tensor of the pack
-        need = max(ops.gemm_workspace_bytes(R, C, m) for R, C in [(16, 256), (8, 512)] for m in range(1, 257))
+        # the GEMM workspace covers any chunk of 1..256 fp32 rows (quantized into it) through up to
+        # three matrices of any quantized tensor shape of the pack
+        need = max(ops.gemm_f32_multi_workspace_bytes([R] * 3, C, m) for R, C in [(16, 256), (8, 512)]
+                   for m in range(1, 257))
+        assert need >= max(ops.gemm_workspace_bytes(R, C, m) for R, C in [(16, 256), (8, 512)] for m in range(1, 257))
         assert eng.gemm_ws.numel() == need + 256
         assert eng.logits.numel() == 16 and eng.row.numel() == 512
     finally:

@@ -283,7 +283,7 @@ def test_gemm_q8k_split_k(dev, orc, ty, R, C, M, S):
     np.testing.assert_array_equal(host(y2)[:, :R], got[:, :R])
 
 
-@pytest.mark.parametrize("C,M", [(4096, 256), (4096, 300), (12288, 130), (2048, 2048)])
+@pytest.mark.parametrize("C,M", [(4096, 256), (4096, 300), (12288, 130), (2048, 2048), (16640, 64)])
 def test_gemm_q8k_multi_matches_single(dev, orc, C, M):
     """A q/k/v-style group (two Q4_K matrices, one Q6_K) in one kq_gemm_q8k_multi_ws call: one
     fragment copy, one launch per type, each matrix keeping the K split of its own call, so every
@@ -311,7 +311,8 @@ def test_gemm_q8k_multi_matches_single(dev, orc, C, M):
             assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C_, ty, xq, M))
 
 
-@pytest.mark.parametrize("C,M,ldx", [(4096, 256, 4096), (4096, 300, 4352), (12288, 130, 12288), (2048, 257, 2048)])
+@pytest.mark.parametrize("C,M,ldx", [(4096, 256, 4096), (4096, 300, 4352), (12288, 130, 12288), (2048, 257, 2048),
+                                    (16640, 40, 16640), (256, 1, 256)])
 def test_gemm_f32_multi_matches_quantize_then_gemm(dev, orc, C, M, ldx):
     """kq_gemm_f32_multi (one launch quantizing the fp32 rows into the workspace and writing the GEMM's
     fragment copy, then the grouped GEMM) equals kq_q8k_quantize followed by kq_gemm_q8k_ws on each
@@ -346,6 +347,23 @@ def test_gemm_f32_multi_matches_quantize_then_gemm(dev, orc, C, M, ldx):
         got = host(y)
         np.testing.assert_array_equal(got[:, :R], host(ref))
         assert np.all(got[:, R:] == -7.0)
+
+
+def test_gemm_q8k_multi_one_type_and_single(dev, orc):
+    """Grouped calls of one matrix, and of three Q6_K matrices (one launch), equal single calls."""
+    C, M = 4352, 200
+    xq = orc.quantize_q8k(kqq.synthetic_activations(M, C, seed=5))
+    xqd = dev_t(xq, dev)
+    for shapes in ([(1024, 12)], [(512, 14), (136, 14), (2048, 14)]):
+        mats = [(dev_t(synth(R, C, ty, 30 + i), dev), R, C, ty) for i, (R, ty) in enumerate(shapes)]
+        ws = torch.empty(ops.gemm_multi_workspace_bytes([R for R, _ in shapes], C, M) + 256, dtype=torch.uint8,
+                         device=dev)
+        ys = [torch.empty((M, R), device=dev) for R, _ in shapes]
+        ops.gemm_q8k_multi(mats, xqd, M, ys, ws)
+        for (w, R, C_, ty), y in zip(mats, ys):
+            ref = torch.empty((M, R), device=dev)
+            ops.gemm_q8k(w, R, C_, ty, xqd, M, ref, ws=ops.gemm_workspace(R, C_, M, dev))
+            np.testing.assert_array_equal(host(y), host(ref))
 
 
 @pytest.mark.parametrize("ty", [12, 14])

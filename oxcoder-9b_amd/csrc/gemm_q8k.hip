@@ -18,10 +18,10 @@
 //   Q4_K: dx * (d * I1 - dmin * I2)          Q6_K: dx * (d * I)
 // (the per-super-block quantity of the CPU reference, with fp32 sums along K).
 //
-// Work split.  A workgroup (4 waves) owns 128 tokens x 64 weight rows; each wave 64 tokens x 32
-// rows (two 32x32 MFMA tiles).  Each thread unpacks 64 of the 256 weights of one weight row into
-// the two LDS planes (rows of 256 B, 16-B chunks XOR-swizzled by row so that 16 consecutive rows
-// hit distinct banks); the planes are double-buffered, so the next super-block is unpacked while
+// Work split.  A workgroup (4 waves) owns 128 tokens x 64 weight rows; each wave 32 tokens x 64
+// rows (two 32x32 MFMA tiles sharing the A operand).  Each thread unpacks 64 of the 256 weights of
+// one weight row into the two LDS planes (rows of 256 B, 16-B chunks XOR-swizzled by row so that
+// 16 consecutive rows hit distinct banks); the planes are double-buffered, so the next super-block is unpacked while
 // the MFMAs of the current one run, with one barrier per super-block.  A workgroup takes 80 KB of
 // LDS and its waves at most 256 VGPRs, so two workgroups share a CU: each SIMD runs two waves and
 // one wave's VALU work (unpack, epilogue) issues while the other's MFMAs run.
@@ -295,14 +295,16 @@ struct GemmGroup {
     int n;
 };
 
-// WN waves along n times WM along m; each wave owns 64 tokens x 32 weight rows (two 32x32 MFMA
-// tiles), the workgroup BM = 64*WM tokens x BN = 32*WN rows.  FRAG: A operands from the
-// fragment-order copy XF, else straight from the Q8_K rows XQ.
-template <int TYPE, int BN, int WN, int WM, bool FRAG>
+// WN waves along n times WM along m; each wave owns MT token tiles x NT = 2/MT weight-row tiles of
+// 32x32 (two MFMA tiles), the workgroup BM = 32*MT*WM tokens x BN = 32*NT*WN rows.  With MT = 1 a wave
+// holds one token tile's A operands (32 VGPRs for a super-block) and uses each for both row tiles,
+// reading twice the B operands from LDS instead.  FRAG: A operands from the fragment-order copy XF,
+// else straight from the Q8_K rows XQ.
+template <int TYPE, int BN, int WN, int WM, bool FRAG, int MT>
 __global__ void __launch_bounds__(64 * WN * WM)
 k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* __restrict__ XF, int M) {
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
-    constexpr int BM = 64 * WM;
+    constexpr int BM = 32 * MT * WM;
     constexpr int NTHR = 64 * WN * WM;
     constexpr int NE = BN / WN;                   // weight rows per wave
     constexpr int NT = NE / 32;                   // 32-column MFMA tiles per wave
@@ -310,7 +312,7 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
     constexpr int XP = NTHR / BM;                 // staging parts per activation row
     constexpr int SHIFT = TYPE == TYPE_Q4_K ? 3 : 8;
     static_assert(PPR == 2 || PPR == 4, "a weight row is split in 2 or 4 parts");
-    static_assert(NT == 1, "one 32-row tile column per wave");
+    static_assert(NT * MT == 2, "two 32x32 tiles per wave");
     __shared__ __attribute__((aligned(16))) GemmBuf<BN, BM> LB0;
     __shared__ __attribute__((aligned(16))) GemmBuf<BN, BM> LB1;
 
@@ -340,13 +342,13 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
 
     // A operand of this lane for K step ks of super-block g: afrag[mt] + g * AG + ks * AK
     constexpr int AG = FRAG ? 8192 : Q8K_BYTES, AK = FRAG ? 1024 : 32;
-    const uint8_t* afrag[2];
+    const uint8_t* afrag[MT];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-        if (FRAG) {   // fragment tile (m0 + 64 wm + 32 mt) / 32
-            afrag[mt] = XF + ((int64_t)(blockIdx.y * (BM / 32) + 2 * wm + mt) * G * 512 + lane) * 16;
+    for (int mt = 0; mt < MT; mt++) {
+        if (FRAG) {   // fragment tile (m0 + 32 MT wm + 32 mt) / 32
+            afrag[mt] = XF + ((int64_t)(blockIdx.y * (BM / 32) + MT * wm + mt) * G * 512 + lane) * 16;
         } else {      // row m, bytes 32 ks + 16 half of its quants
-            int m = m0 + 64 * wm + 32 * mt + l32;
+            int m = m0 + 32 * MT * wm + 32 * mt + l32;
             m = m < M ? m : M - 1;
             afrag[mt] = XQ + m * xrow + 4 + 16 * half;
         }
@@ -359,20 +361,20 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
     const int pr = n0 + prow < R ? n0 + prow : R - 1;
     const uint8_t* wrow = W + ((int64_t)(pr >> 3) * G * 8 + (pr & 7)) * BS;   // block (pr, g) = wrow + g*8*BS
 
-    float yacc[2][16];
+    float yacc[2][16];                      // tile t = mt * NT + nt
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int a = 0; a < 16; a++) yacc[mt][a] = 0.0f;
+        for (int a = 0; a < 16; a++) yacc[t][a] = 0.0f;
 
     // ---- prologue: super-block 0 staged, super-block 1's raw bytes in registers
     RawW<TYPE, PPR> raw;
     RawX<XP> rx;
-    v4i afr[2][8];
+    v4i afr[MT][8];
     load_raw(raw, wrow + (int64_t)gbeg * 8 * BS, pi);
     load_x(rx, xstage + (int64_t)gbeg * Q8K_BYTES, xp);
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
             afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gbeg * AG + ks * AK));
@@ -385,80 +387,82 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
     }
     __syncthreads();
 
-    const int nrow0 = wn * NE + l32;        // this lane's B row (weight row within the tile)
-    // One super-block step; the LDS buffer index is a compile-time constant (the loop is unrolled
-    // by two) so the compiler can tell the next buffer's stores from the current buffer's loads and
-    // overlap the unpack with the MFMAs.
+    int nrow0[NT];                          // this lane's B rows (weight rows within the tile)
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) nrow0[nt] = wn * NE + 32 * nt + l32;
     auto step = [&](auto cur_c, int g) {
         constexpr int cur = decltype(cur_c)::value;
         GemmBuf<BN, BM>& Lc = cur ? LB1 : LB0;   // read this step
         GemmBuf<BN, BM>& Ln = cur ? LB0 : LB1;   // filled for the next step
         const int gn = g + 1 < gend ? g + 1 : gend - 1;
         const int g2 = g + 2 < gend ? g + 2 : gend - 1;
-
-        // ---- stage super-block g+1 into the other buffer (last iteration: a harmless repeat),
-        //      then fetch the raw bytes of g+2
         unpack(raw, pi, prow, Ln);
         stage_x<TYPE>(rx, mr, xp, Ln);
         load_raw(raw, wrow + (int64_t)g2 * 8 * BS, pi);
         load_x(rx, xstage + (int64_t)g2 * Q8K_BYTES, xp);
 
-        // ---- hi sweep: acc = A . H, interleaved by the scheduler with the unpack above
         v16i acc[2];
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
-            const v4i b = *reinterpret_cast<const v4i*>(Lc.wh + swz(nrow0, 2 * ks + half));
+            v4i b[NT];
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-                acc[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b, ks == 0 ? v16i{} : acc[mt], 0, 0, 0);
+            for (int nt = 0; nt < NT; nt++) b[nt] = *reinterpret_cast<const v4i*>(Lc.wh + swz(nrow0[nt], 2 * ks + half));
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    acc[mt * NT + nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt],
+                                                                             ks == 0 ? v16i{} : acc[mt * NT + nt], 0, 0, 0);
         }
         __builtin_amdgcn_iglp_opt(1);
         __builtin_amdgcn_sched_barrier(0);
 
-        // epilogue of token tile mt of super-block g
-        auto epilogue = [&](int mt) {
+        auto epilogue = [&](int mt, int nt) {
+            const int t = mt * NT + nt;
             f32x4 dxv[4];
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                dxv[q] = *reinterpret_cast<const f32x4*>(&Lc.dx[64 * wm + 32 * mt + 8 * q + 4 * half]);
-            const int ml = 64 * wm + 32 * mt + l32;
-            const float dn = Lc.d[nrow0];
+                dxv[q] = *reinterpret_cast<const f32x4*>(&Lc.dx[32 * MT * wm + 32 * mt + 8 * q + 4 * half]);
+            const int ml = 32 * MT * wm + 32 * mt + l32;
+            const float dn = Lc.d[nrow0[nt]];
             if (TYPE == TYPE_Q4_K) {
-                const float dmn = Lc.dm[nrow0];
-                const v8h bm = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&Lc.wmin[nrow0 * 8 + 4 * half]));
+                const float dmn = Lc.dm[nrow0[nt]];
+                const v8h bm = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&Lc.wmin[nrow0[nt] * 8 + 4 * half]));
                 const v8h am = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&Lc.xmin[ml * 8 + 4 * half]));
                 const v16f cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, v16f{}, 0, 0, 0);   // -I2
 #pragma unroll
                 for (int a = 0; a < 16; a++) {
-                    const float t = __builtin_fmaf(dmn, cm[a], __fmul_rn(dn, (float)acc[mt][a]));
-                    yacc[mt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], t, yacc[mt][a]);
+                    const float tt = __builtin_fmaf(dmn, cm[a], __fmul_rn(dn, (float)acc[t][a]));
+                    yacc[t][a] = __builtin_fmaf(dxv[a >> 2][a & 3], tt, yacc[t][a]);
                 }
             } else {
 #pragma unroll
                 for (int a = 0; a < 16; a++)
-                    yacc[mt][a] = __builtin_fmaf(dxv[a >> 2][a & 3], __fmul_rn(dn, (float)acc[mt][a]), yacc[mt][a]);
+                    yacc[t][a] = __builtin_fmaf(dxv[a >> 2][a & 3], __fmul_rn(dn, (float)acc[t][a]), yacc[t][a]);
             }
         };
 
-        // ---- lo sweep: acc = 2^SHIFT acc + A . L with both token tiles' accumulator chains
-        //      interleaved; each K step's A fragments are replaced by super-block g+1's right after
-        //      their last use; then both epilogues (the other wave of the SIMD keeps the MFMA pipe
-        //      busy meanwhile)
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int a = 0; a < 16; a++) acc[mt][a] <<= SHIFT;
+            for (int a = 0; a < 16; a++) acc[t][a] <<= SHIFT;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
-            const v4i b = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0, 2 * ks + half));
+            v4i b[NT];
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                acc[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b, acc[mt], 0, 0, 0);
+            for (int nt = 0; nt < NT; nt++) b[nt] = *reinterpret_cast<const v4i*>(Lc.wl + swz(nrow0[nt], 2 * ks + half));
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    acc[mt * NT + nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[mt][ks], b[nt], acc[mt * NT + nt], 0, 0, 0);
                 afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
             }
         }
-        epilogue(0);
-        epilogue(1);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) epilogue(mt, nt);
         __syncthreads();
     };
     for (int g = gbeg; g < gend; g += 2) {
@@ -466,14 +470,16 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
         if (g + 1 < gend) step(std::integral_constant<int, 1>{}, g + 1);
     }
 
-    // ---- store
-    const int n = n0 + nrow0;
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int a = 0; a < 16; a++) {
-            const int m = m0 + 64 * wm + 32 * mt + (a >> 2) * 8 + half * 4 + (a & 3);
-            if (m < M && n < R) Yo[(int64_t)m * ldo + n] = yacc[mt][a];
+        for (int nt = 0; nt < NT; nt++) {
+            const int n = n0 + nrow0[nt];
+#pragma unroll
+            for (int a = 0; a < 16; a++) {
+                const int m = m0 + 32 * MT * wm + 32 * mt + (a >> 2) * 8 + half * 4 + (a & 3);
+                if (m < M && n < R) Yo[(int64_t)m * ldo + n] = yacc[mt * NT + nt][a];
+            }
         }
 }
 
@@ -582,16 +588,16 @@ size_t gemm_q8k_group_workspace(int n, const int* R, int C, int M) {
 
 size_t gemm_q8k_workspace(int R, int C, int M) { return gemm_q8k_group_workspace(1, &R, C, M); }
 
-template <int TYPE, int BN, int WN, int WM>
+template <int TYPE, int BN, int WN, int WM, int MT>
 static void launch_tile(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, const uint8_t* xf, int M,
                         const int* S, hipStream_t s) {
-    constexpr int BM = 64 * WM;
+    constexpr int BM = 32 * MT * WM;
     static_assert(BN == GM_TN && BM == GM_TM, "the split rule assumes these tiles");
     dim3 grid(wgs, (M + BM - 1) / BM), block(64 * WN * WM);
     if (xf)
-        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true>), grid, block, 0, s, gg, G, xq, xf, M);
+        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true, MT>), grid, block, 0, s, gg, G, xq, xf, M);
     else
-        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false>), grid, block, 0, s, gg, G, xq, xf, M);
+        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false, MT>), grid, block, 0, s, gg, G, xq, xf, M);
     // one reduce launch for the matrices that split K
     ReduceGroup rg{};
     int blks = 0;
@@ -615,9 +621,12 @@ static void launch_type(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, 
                         const int* S, hipStream_t s) {
     // 128 tokens x 64 weight rows per workgroup of 4 waves (80 KB of LDS, at most 256 VGPRs), so two
     // workgroups share a CU and each SIMD holds two waves: one wave's unpack and epilogue run under
-    // the other's MFMAs.  (Measured against 128 x 128 tiles, one wave per SIMD, 4-8 waves per
+    // the other's MFMAs.  Each wave takes 32 tokens x all 64 rows (MT = 1): half the A-operand
+    // loads of 64 tokens x 32 rows (MT = 2), for twice the B reads from LDS; 12288x4096 Q4_K at
+    // M = 2048 / 512 / 256: 285 / 76.8 / 49.3 -> 270 / 73.8 / 45.7 us, 4096x12288 Q6_K 311 / 91.2
+    // -> 300 / 88.1 us.  (Measured against 128 x 128 tiles, one wave per SIMD, 4-8 waves per
     // workgroup: 289-317 against 331-379 us at M = 2048.)
-    launch_tile<TYPE, 64, 2, 2>(gg, wgs, G, xq, xf, M, S, s);
+    launch_tile<TYPE, 64, 1, 4, 1>(gg, wgs, G, xq, xf, M, S, s);
 }
 
 // ------------------------------------------------------------------ the no-allocation form

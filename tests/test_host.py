@@ -183,6 +183,52 @@ def test_gemm_workspace_follows_the_split_rule():
         assert lib.kq_gemm_q8k_workspace(R, C, M) == 0, (R, C, M)
 
 
+def test_grouped_gemm_workspace_and_argument_checks():
+    """kq_gemm_q8k_multi_workspace / kq_gemm_f32_multi_workspace (host only): the fragment copy once
+    plus each matrix's own partial planes (the f32 form adds the chunk's Q8_K rows, 256-byte
+    aligned, in front); invalid sizes give 0; bad calls return KQ_ERR_ARG before any launch."""
+    from kq import _lib
+    lib = _lib.kq()
+    I3 = ctypes.c_int * 3
+    for Rs, C, M in [((4096, 1024, 1024), 4096, 256), ((12288, 12288, 12288), 4096, 300),
+                     ((4096, 8, 136), 12288, 130), ((2048, 2048, 2048), 2048, 2048)]:
+        frag = -(-(-(-M // 256) * 256 * C) // 256) * 256
+        want = frag + sum(lib.kq_gemm_q8k_workspace(R, C, M) - frag for R in Rs)
+        assert lib.kq_gemm_q8k_multi_workspace(3, I3(*Rs), C, M) == want
+        q8k = -(-M * (C // 256) * 292 // 256) * 256
+        assert lib.kq_gemm_f32_multi_workspace(3, I3(*Rs), C, M) == q8k + want
+        assert lib.kq_gemm_q8k_multi_workspace(1, I3(*Rs), C, M) == lib.kq_gemm_q8k_workspace(Rs[0], C, M)
+    for n, Rs, C, M in [(0, (8, 8, 8), 256, 1), (4, (8, 8, 8), 256, 1), (2, (8, 12, 8), 256, 1),
+                        (1, (8, 8, 8), 300, 1), (1, (8, 8, 8), 256, 0)]:
+        assert lib.kq_gemm_q8k_multi_workspace(n, I3(*Rs), C, M) == 0
+        assert lib.kq_gemm_f32_multi_workspace(n, I3(*Rs), C, M) == 0
+    P = ctypes.c_void_p * 3
+    L = ctypes.c_int64 * 3
+    w, y = P(4096, 4096, 4096), P(4096, 4096, 4096)
+    R, T, ld = I3(64, 64, 64), I3(12, 14, 12), L(64, 64, 64)
+    cases = [
+        (lambda: lib.kq_gemm_q8k_multi_ws(4, w, R, 256, T, ctypes.c_void_p(4096), 8, y, ld, ctypes.c_void_p(4096),
+                                          1 << 20, None), "n=4"),
+        (lambda: lib.kq_gemm_q8k_multi_ws(2, None, R, 256, T, ctypes.c_void_p(4096), 8, y, ld,
+                                          ctypes.c_void_p(4096), 1 << 20, None), "NULL array"),
+        (lambda: lib.kq_gemm_q8k_multi_ws(3, w, R, 256, I3(12, 13, 12), ctypes.c_void_p(4096), 8, y, ld,
+                                          ctypes.c_void_p(4096), 1 << 20, None), "type 13"),
+        (lambda: lib.kq_gemm_q8k_multi_ws(3, w, R, 256, T, ctypes.c_void_p(4096), 8, y, ld, ctypes.c_void_p(4100),
+                                          1 << 20, None), "256-byte aligned"),
+        (lambda: lib.kq_gemm_q8k_multi_ws(3, w, R, 256, T, ctypes.c_void_p(4096), 8, y, ld, ctypes.c_void_p(4096),
+                                          16, None), "workspace of 16 bytes"),
+        (lambda: lib.kq_gemm_f32_multi(3, w, R, 256, T, ctypes.c_void_p(4096), 100, 8, y, ld, ctypes.c_void_p(4096),
+                                       1 << 20, None), "ldx=100"),
+        (lambda: lib.kq_gemm_f32_multi(3, w, R, 256, T, None, 256, 8, y, ld, ctypes.c_void_p(4096), 1 << 20, None),
+         "x is NULL"),
+        (lambda: lib.kq_gemm_f32_multi(3, w, R, 256, T, ctypes.c_void_p(4096), 256, 8, y, L(64, 8, 64),
+                                       ctypes.c_void_p(4096), 1 << 20, None), "ldy=8"),
+    ]
+    for call, msg in cases:
+        assert call() == _lib.KQ_ERR_ARG, msg
+        assert msg in lib.kq_last_error().decode(), (msg, lib.kq_last_error())
+
+
 def test_static_gemm_limit_checked_on_the_host():
     """kq_gemm_q8k_static rejects a GEMM whose workspace exceeds its static array before touching a
     device (host only); a 256-token chunk of every 9B-model matrix fits the array."""

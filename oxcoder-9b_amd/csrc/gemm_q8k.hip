@@ -401,6 +401,10 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
         load_raw(raw, wrow + (int64_t)g2 * 8 * BS, pi);
         load_x(rx, xstage + (int64_t)g2 * Q8K_BYTES, xp);
 
+        // Q6_K: the wave's MFMA sweeps at raised issue priority, so the other wave of the SIMD runs its
+        // (heavier) unpack and epilogue in the MFMAs' shadow (4096x12288 at M = 2048 / 512: 303 / 90.1
+        // -> 294 / 87.5 us; for Q4_K, whose unpack is interleaved into the hi sweep, it was slower)
+        if constexpr (TYPE == TYPE_Q6_K) __builtin_amdgcn_s_setprio(3);
         v16i acc[2];
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
@@ -459,6 +463,7 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
                 afr[mt][ks] = __builtin_bit_cast(v4i, ld16_a4(afrag[mt] + (int64_t)gn * AG + ks * AK));
             }
         }
+        if constexpr (TYPE == TYPE_Q6_K) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll

@@ -16,7 +16,10 @@ for each name, ``outs[i][:R] = W_name @ x`` on the current stream, asynchronousl
 
 ``gemv_batch`` (speculative verify, N <= 16 rows) and ``gemm`` (prefill chunk, any M) extend the
 same contract to several activation rows: X is [N][C] fp32, each out is [N][R] (row stride
-``out.stride(0)``), the batched layout of the ternary engine's k_tc_mv (tc.cu:306-310).
+``out.stride(0)``), the batched layout of the ternary engine's k_tc_mv (tc.cu:306-310).  In
+``"q8k"`` mode they run the batched Q8_K GEMV and the prefill GEMM; in ``"f32"`` mode every row goes
+through the fp32 GEMV as one decode step would (the reference's Q4 engine prefills token by token,
+gpu4.py:109-110), so each output row equals ``gemv`` on that row bit for bit.
 
 The producers of the GEMV inputs write the Q8_K activation directly: ``rmsfold_q8k`` (the
 residual add + RMSNorm of Engine.rmsfold, gpu4.py:104-106 / q4_rms, q4.cu:39-46) and
@@ -231,6 +234,14 @@ class Engine:
         return {"libkq": _lib.kq().kq_source_hash().decode(), "mode": self.mode,
                 "weights": "kindi-q4-v1: Q4_K/Q6_K row tiles"}
 
+    def _rows_f32(self, mats, X, outs):
+        """Mode "f32": every row of X through the fp32 GEMV (kq_gemv_multi), three matrices a launch."""
+        for n in range(X.shape[0]):
+            ys = [y[n] if y.dim() == 2 else y[n * R:(n + 1) * R] for (_, R, _, _), y in zip(mats, outs)]
+            for i in range(0, len(mats), 3):
+                ops.gemv_multi(mats[i:i + 3], X[n], ys[i:i + 3])
+        return 1
+
     def gemv_batch(self, names, X, outs):
         """Speculative-verify GEMV: X [N][C], N <= 16; out[n][r] bit-identical to gemv on row n."""
         N, C = X.shape
@@ -241,6 +252,8 @@ class Engine:
             if C_ != C:
                 raise ValueError("column count mismatch")
             self._check_out(y, R, N)
+        if self.mode == "f32":
+            return self._rows_f32(mats, X, outs)
         xq = self._quantize(X, C)
         for (w, R, C_, ty), y in zip(mats, outs):
             ops.gemv_q8k(w, R, C_, ty, xq, N, y, y.stride(0) if y.dim() == 2 else R)
@@ -252,7 +265,8 @@ class Engine:
         a time through kq_gemm_f32_multi, which quantizes the chunk once into the engine's GEMM
         workspace (Q8_K rows and the GEMM's fragment copy in one launch) and runs one GEMM launch per
         weight type.  Chunk results equal kq_q8k_quantize then one kq_gemm_q8k_ws call per matrix on
-        that chunk, bit for bit.  Allocates nothing."""
+        that chunk, bit for bit.  In "f32" mode every row goes through the fp32 GEMV instead, as in
+        gemv_batch.  Allocates nothing."""
         M, C = X.shape
         if not self.chunk:
             raise ValueError("chunked prefill is off (chunk 0): use feed_rows or gemv_batch")
@@ -261,6 +275,8 @@ class Engine:
             if C_ != C:
                 raise ValueError("column count mismatch")
             self._check_out(y, R, M)
+        if self.mode == "f32":
+            return self._rows_f32(mats, X, outs)
         if C > self.max_cols:
             raise ValueError("input of %d columns exceeds the engine workspace (%d)" % (C, self.max_cols))
         for m0 in range(0, M, self.chunk):

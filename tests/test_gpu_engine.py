@@ -187,6 +187,27 @@ def test_engine_feed_rows_dispatch(layer, dev):
     assert len(fp["libkq"]) == 16 and fp["mode"] == "q8k"
 
 
+def test_engine_f32_mode_batched_rows_are_decode_rows(layer, dev):
+    """Mode "f32" keeps the reference's numerics on the batched paths too: gemv_batch, feed_rows
+    (batched and prefill sizes) and gemm give every row bit-identical to gemv on that row (the
+    reference's Q4 engine prefills token by token, gpu4.py:109-110), into 2-D and flat outputs."""
+    w, host = layer
+    eng = Engine(w, mode="f32")
+    names = ["attn_q", "attn_k", "attn_v"]
+    X = torch.from_numpy(kqq.synthetic_activations(20, 4096, seed=21)).to(dev)
+    single = {n: torch.empty((20, host[n][1]), device=dev) for n in names}
+    for r in range(20):
+        eng.gemv(names, X[r], [single[n][r] for n in names])
+    for call, rows in ((eng.gemv_batch, 6), (eng.feed_rows, 6), (eng.feed_rows, 20), (eng.gemm, 20)):
+        outs = [torch.full((rows, host[n][1]), -1.0, device=dev) for n in names]
+        assert call(names, X[:rows], outs) == 1
+        for n, y in zip(names, outs):
+            assert torch.equal(y, single[n][:rows]), (call.__name__, rows, n)
+    flat = torch.empty(20 * 1024, device=dev)
+    eng.gemm(["attn_k"], X, [flat])
+    assert torch.equal(flat.view(20, 1024), single["attn_k"])
+
+
 def test_engine_prefill_gemm_split_k_layer(layer, dev):
     """A 48-token prefill chunk through Engine.gemm for matrices of different R sharing one
     workspace: q/k/v (grids of 64 and 16 tiles: K split 4 ways) and down (K split 8 ways).  Every

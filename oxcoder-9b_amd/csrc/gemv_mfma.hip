@@ -14,7 +14,8 @@
 // planes: Q4_K sc = 8a + b, planes a*q and b*q (I1 = 8*(x.H) + (x.L)); Q6_K w = sc*(q - 32),
 // v = w + 128, planes high byte of v and low byte of v ^ 0x80 (I = 256*(x.H) + (x.L)).  The Q4_K
 // min term is one v_mfma_f32_16x16x16_f16 with exact small-integer operands [B_s >> 6, B_s & 63]
-// and [-64 m_s, -m_s], which returns -I2 exactly.
+// and [-64 m_s, -m_s], which returns -I2 exactly.  Q6_K up to 8 tokens takes a second form
+// (k_gemv_mfma_q6, below): raw codes against sub-block-phased activations, no planes.
 //
 // MFMA lanes: lane l serves token (A operand) and weight row (B operand) l & 15 and K slots
 // 16q .. 16q+15 of each step, q = l >> 4.  Outputs: lane l holds tokens 4q + j (j = 0..3) of row
@@ -36,6 +37,16 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+#ifndef KQ_GEMV_MFMA_Q6_PLANES
+#define KQ_GEMV_MFMA_Q6_PLANES 0   // 1: Q6_K through the two-plane form instead of sub-block phases
+#endif
+#ifndef KQ_Q6P_FP1
+#define KQ_Q6P_FP1 4   // super-blocks in flight per wave, Q6_K phase form, 1-4 tokens
+#endif
+#ifndef KQ_Q6P_FP2
+#define KQ_Q6P_FP2 2   // the same, 5-8 tokens
+#endif
 
 constexpr int MV_ROWS = 16;     // weight rows per workgroup
 constexpr int MV_CHUNK = 4;     // super-blocks per wave
@@ -300,6 +311,191 @@ k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     }
 }
 
+// ------------------------------------------------------------------ Q6_K by sub-block phases
+// Q6_K's scale changes every 16 columns.  Instead of folding it into two weight planes, this form
+// keeps the raw 6-bit codes (0..63) as the MFMA's B operand and separates the sub-blocks on the A
+// side.  K group q (slots 16q .. 16q+15) of step s carries sub-block j(s, q) = 8(q >> 1) + (q & 1)
+// + 2s, so lane q of a weight row reads ql bytes 64h + 16b and 64h + 32 + 16b, qh bytes 32h + 16b
+// and the scales (h = q >> 1, b = q & 1), 52 bytes, and step s takes nibble s >> 1 of ql word s & 1
+// and bit pair s of qh.  A row a = 4t + p (token t of a group of four, phase p) holds token t's
+// activations in K group (p + s) & 3 only, zeros elsewhere, so output row 4t + p of step s is the
+// 16-element sum S of sub-block j(s, (p + s) & 3) alone, and every A lane carries data in exactly
+// one step (its 16 bytes are loaded once and selected per step).  Lane l (q = l >> 4) then holds,
+// for weight row l & 15 and token 4 gi + q, the sums of the step's four sub-blocks, and forms
+//   I = sum_j sc_j * S_j - 32 * sum_j sc_j * b_j
+// (b_j = the Q8_K bsums, sc_j the signed scales): the first sum with 24-bit multiply-adds
+// (|S_j| <= 16 * 128 * 63 < 2^23), the second with one v_mfma_f32_16x16x16_f16 whose operands and
+// partial sums are exact small integers (|b_j| <= 2032, |sc_j| <= 128, |sum| < 2^23).  I is the
+// GEMV's integer, so the per-super-block value and every row are bit-identical to the one-token
+// GEMV; the unpack is ~3.3 VALU per 4 codes instead of ~13 for the planes, and the smaller
+// operands let all four super-blocks of a wave be in flight at once.
+constexpr int MV_OOB = 0x40000000;   // buffer offset beyond any activation buffer: the load returns 0
+
+__device__ __forceinline__ constexpr int q6p_sub(int s, int q) { return 8 * (q >> 1) + (q & 1) + 2 * s; }
+
+// Raw words of one super-block for lane q: ql bytes 64h + 16b and 64h + 32 + 16b, qh bytes
+// 128 + 32h + 16b, scales, each 16-byte field with the dword after it (funnel-shifted by sh).
+struct MvW6 { u32x4 ql[2], qh, sc; uint32_t qle[2], qhe, sce, sh; };
+
+template <int NG> struct MvX6 {
+    u32x4 a[NG];      // token 4 gi + (l & 15) / 4, sub-block j((q - p) & 3, q): its one active step
+    u32x2 bs[NG];     // bsums 4q .. 4q+3 of token 4 gi + (l & 15) / 4 where l & 3 == 0; else 0
+    float dx[NG];     // d of token 4 gi + q
+};
+
+// The last word read (bytes 208..211 from the aligned base) passes the block end by 2 bytes only
+// for blocks starting at 0 (mod 4), which are never row 7 of a tile column.
+__device__ __forceinline__ void mv6_load(MvW6& w, const uint8_t* bk, int q) {
+    w.sh = uint32_t(reinterpret_cast<uintptr_t>(bk) & 3);
+    const uint8_t* b4 = bk - w.sh;
+    const int h = q >> 1, b = q & 1;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        w.ql[c] = ld16_a4(b4 + 64 * h + 32 * c + 16 * b);
+        w.qle[c] = ld4(b4 + 64 * h + 32 * c + 16 * b + 16);
+    }
+    w.qh = ld16_a4(b4 + 128 + 32 * h + 16 * b);
+    w.qhe = ld4(b4 + 144 + 32 * h + 16 * b);
+    w.sc = ld16_a4(b4 + 192);
+    w.sce = ld4(b4 + 208);
+}
+
+template <int NG>
+__device__ __forceinline__ void mv6_values(const MvW6& w, const MvX6<NG>& x, int q, int p, float (&v)[NG]) {
+    const uint32_t sh = w.sh;
+    const u32x4 QL[2] = {mv_funnel(w.ql[0], w.qle[0], sh), mv_funnel(w.ql[1], w.qle[1], sh)};
+    const u32x4 QH = mv_funnel(w.qh, w.qhe, sh);
+    const u32x4 SC = mv_funnel(w.sc, w.sce, sh);   // scale of sub-block j = byte j & 3 of dword j >> 2
+    const float d = f16_lo(w.sce >> (8 * sh));
+    const uint32_t hw[4] = {QH.x, QH.y, QH.z, QH.w};
+    v4i bq[4];   // B of step s: codes of sub-block j(s, q), 6-bit, as bytes
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const u32x4 L = QL[s & 1];
+        const uint32_t lw[4] = {L.x, L.y, L.z, L.w};
+        uint32_t c[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lq = (lw[i] >> (4 * (s >> 1))) & 0x0f0f0f0fu;
+            const uint32_t hq = s < 2 ? hw[i] << (4 - 2 * s) : hw[i] >> (2 * s - 4);   // bit pair s to bits 4..5
+            c[i] = (hq & 0x30303030u) | lq;
+        }
+        bq[s] = v4i{(int)c[0], (int)c[1], (int)c[2], (int)c[3]};
+    }
+    // B of the b term: scales of sub-blocks 4q .. 4q+3 as fp16
+    const uint32_t scq = q == 0 ? SC.x : q == 1 ? SC.y : q == 2 ? SC.z : SC.w;
+    const v4h bsc = __builtin_bit_cast(v4h, u32x2{mv_pk_f16((float)sbyte(scq, 0), (float)sbyte(scq, 1)),
+                                                  mv_pk_f16((float)sbyte(scq, 2), (float)sbyte(scq, 3))});
+    const uint32_t scw[4] = {SC.x, SC.y, SC.z, SC.w};
+    const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) {
+        const v4i xa = __builtin_bit_cast(v4i, x.a[gi]);
+        int I = 0;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const v4i a = ((p + s) & 3) == q ? xa : zero;    // this lane's phase owns K group q at step s
+            const v4i S = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq[s], zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {          // output row 4q + r: phase r, sub-block j(s, (r + s) & 3)
+                const int j = q6p_sub(s, (r + s) & 3);
+                I += sbyte(scw[j >> 2], j & 3) * ((S[r] << 8) >> 8);   // 24-bit operands
+            }
+        }
+        const uint32_t b0 = x.bs[gi].x, b1 = x.bs[gi].y;
+        const v4h bb = __builtin_bit_cast(v4h, u32x2{mv_pk_f16((float)shalf(b0, 0), (float)shalf(b0, 1)),
+                                                     mv_pk_f16((float)shalf(b1, 0), (float)shalf(b1, 1))});
+        const v4f cb = __builtin_amdgcn_mfma_f32_16x16x16f16(bb, bsc, v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        v[gi] = q6k_value(d, x.dx[gi], I - 32 * (int)cb[0]);
+    }
+}
+
+// Workgroup and merge as k_gemv_mfma; NG groups of four tokens (N <= 4 NG) share each unpack; FP of
+// the wave's four super-blocks are in flight before the first is used.
+template <int NG, int LB, int FP>
+__global__ void __launch_bounds__(LB)
+k_gemv_mfma_q6(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
+    constexpr int BS = Q6K_BYTES;
+    __shared__ float part[16][16][MV_ROWS];            // [chunk][token][row] chunk sums
+    const int lane = threadIdx.x & 63;
+    const int chunk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nchunks = blockDim.x >> 6;
+    const int q = lane >> 4, l16 = lane & 15;
+
+    const int wg = blockIdx.x;
+    const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
+    const int R = mg.R[m];
+    const int row0 = (wg - mg.first[m]) * MV_ROWS;
+    int row = row0 + l16;
+    row = row < R ? row : R - 1;                       // rows past R are loaded clamped, not stored
+    const int64_t col_bytes = 8 * BS;
+    const uint8_t* wrow = mg.w[m] + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
+    const int xrow = G * Q8K_BYTES;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(XQ), 0, N * xrow, 0x00020000);
+    const int t = l16 >> 2, p = lane & 3;
+    const int ja = q6p_sub((q - p) & 3, q);            // the sub-block of this lane's active step
+    int aoff[NG], boff[NG];
+    const uint8_t* xd[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) {
+        const int tok = 4 * gi + t;
+        aoff[gi] = tok < N ? tok * xrow + 4 + 16 * ja : MV_OOB;
+        boff[gi] = p == 0 && tok < N ? tok * xrow + 260 + 8 * q : MV_OOB;
+        const int n = 4 * gi + q;
+        xd[gi] = XQ + (int64_t)(n < N ? n : N - 1) * xrow;
+    }
+
+    const int g0 = MV_CHUNK * chunk;
+    auto load = [&](int s, MvW6& ww, MvX6<NG>& xx) {
+        const int g = g0 + s < G ? g0 + s : G - 1;
+        mv6_load(ww, wrow + (int64_t)g * col_bytes, q);
+        const int go = g * Q8K_BYTES;
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            xx.a[gi] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff[gi] + go, 0, 0));
+            xx.bs[gi] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(xr, boff[gi] + go, 0, 0));
+            xx.dx[gi] = __builtin_bit_cast(float, ld4(xd[gi] + go));
+        }
+    };
+    float v[MV_CHUNK][NG];
+    MvW6 w[FP];
+    MvX6<NG> x[FP];
+#pragma unroll
+    for (int s = 0; s < FP; s++) load(s, w[s], x[s]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < MV_CHUNK; s++) {
+        float vv[NG];
+        mv6_values<NG>(w[s % FP], x[s % FP], q, p, vv);
+        const bool valid = g0 + s < G;          // columns past G contribute +0
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) v[s][gi] = valid ? vv[gi] : 0.0f;
+        if (s + FP < MV_CHUNK) load(s + FP, w[s % FP], x[s % FP]);
+    }
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++)
+        part[chunk][4 * gi + q][l16] = __fadd_rn(__fadd_rn(v[0][gi], v[1][gi]), __fadd_rn(v[2][gi], v[3][gi]));
+    __syncthreads();
+
+    const int passes = (G + 15) / 16;
+    for (int idx = threadIdx.x; idx < N * MV_ROWS; idx += blockDim.x) {
+        const int n = idx / MV_ROWS, r = idx - n * MV_ROWS;
+        if (row0 + r >= R) continue;
+        PassTree tr;
+        tree_init(tr);
+        for (int ps = 0; ps < passes; ps++) {
+            float c[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int cc = 4 * ps + k;
+                c[k] = cc < nchunks ? part[cc][n][r] : 0.0f;
+            }
+            tree_push(tr, __fadd_rn(__fadd_rn(c[0], c[1]), __fadd_rn(c[2], c[3])));
+        }
+        mg.y[m][(int64_t)n * mg.ldy[m] + row0 + r] = tree_final(tr);
+    }
+}
+
 template <int TYPE, int LB, bool PRE_ALL, bool SB>
 static void launch_mv(const MvGroup& mg, int wgs, const uint8_t* xq, int N, int G, hipStream_t s) {
     const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
@@ -311,7 +507,10 @@ static void launch_mv(const MvGroup& mg, int wgs, const uint8_t* xq, int N, int 
 // Schedules by shape, each the fastest measured for its case (12288x4096 and 4096x12288 Q4_K,
 // 4096x12288 and 1024x4096 Q6_K; N = 3..16):
 //   Q4_K, G <= 16: all four super-blocks in flight (3 waves per SIMD);
-//   Q4_K, G > 16 and Q6_K: two in flight, behind the barrier.
+//   Q4_K, G > 16 and Q6_K beyond 8 tokens or 48 super-blocks: two in flight, behind the barrier;
+//   Q6_K up to 8 tokens and 48 super-blocks: the phase form, all four super-blocks in flight for
+//   up to 4 tokens, two for 5..8 (4096x12288 at N = 3 / 4 / 5 / 8: 15.3 / 15.3 / 15.3 / 16.1 ->
+//   12.7 / 12.8 / 14.0 / 14.4 us; 4096x4096 at N = 4: 7.0 -> 5.9 us).
 void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
                             int N, float* const* y, const int64_t* ldy, hipStream_t s) {
     const int G = C / QK;
@@ -330,8 +529,15 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
         if (G <= 16) launch_mv<TYPE_Q4_K, 256, true, true>(mg, wgs, xq, N, G, s);
         else if (G <= 48) launch_mv<TYPE_Q4_K, 768, false, true>(mg, wgs, xq, N, G, s);
         else launch_mv<TYPE_Q4_K, 1024, false, true>(mg, wgs, xq, N, G, s);
-    } else {
+    } else if (KQ_GEMV_MFMA_Q6_PLANES || N > 8 || G > 48) {
+        // beyond 8 tokens the phase form needs more registers than 3 waves per SIMD leave (spills);
+        // beyond 48 super-blocks a workgroup has 16 waves, 4 per SIMD (128 registers: spills too)
         launch_mv<TYPE_Q6_K, 1024, false, true>(mg, wgs, xq, N, G, s);
+    } else {
+        const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
+        const dim3 grid(wgs), block(64 * nchunks);
+        if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_q6<1, 768, KQ_Q6P_FP1>), grid, block, 0, s, mg, xq, N, G);
+        else hipLaunchKernelGGL((k_gemv_mfma_q6<2, 768, KQ_Q6P_FP2>), grid, block, 0, s, mg, xq, N, G);
     }
 }
 

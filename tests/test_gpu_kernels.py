@@ -178,7 +178,7 @@ def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
     for n in range(16):
         ops.gemv_q8k(W, R, C, ty, xqd[n:n + 1], 1, single[n])
     s = host(single)
-    for N in (2, 3, 4, 5, 8, 13, 16):
+    for N in (2, 3, 4, 5, 7, 8, 9, 13, 16):
         yb = torch.empty((N, R + 8), device=dev)
         ops.gemv_q8k(W, R, C, ty, xqd[:N], N, yb, R + 8)
         np.testing.assert_array_equal(host(yb)[:, :R], s[:N])

@@ -1,4 +1,4 @@
-// Small-batch GEMV (speculative verify, 2..16 tokens) on int8 MFMA for gfx950.
+// Small-batch GEMV (speculative verify, 2..16 tokens; one token for some shapes) on int8 MFMA for gfx950.
 //
 // A wave owns 16 weight rows x 4 consecutive super-blocks (a "chunk") for all tokens: per
 // super-block it forms the exact integers of the GEMV (Q4_K: I1 = sum sc_s*S_s and
@@ -14,8 +14,8 @@
 // planes: Q4_K sc = 8a + b, planes a*q and b*q (I1 = 8*(x.H) + (x.L)); Q6_K w = sc*(q - 32),
 // v = w + 128, planes high byte of v and low byte of v ^ 0x80 (I = 256*(x.H) + (x.L)).  The Q4_K
 // min term is one v_mfma_f32_16x16x16_f16 with exact small-integer operands [B_s >> 6, B_s & 63]
-// and [-64 m_s, -m_s], which returns -I2 exactly.  Q6_K up to 8 tokens takes a second form
-// (k_gemv_mfma_q6, below): raw codes against sub-block-phased activations, no planes.
+// and [-64 m_s, -m_s], which returns -I2 exactly.  Up to 4 (Q4_K) or 8 (Q6_K) tokens a second form
+// is used (k_gemv_mfma_ph, below): raw codes against sub-block-phased activations, no planes.
 //
 // MFMA lanes: lane l serves token (A operand) and weight row (B operand) l & 15 and K slots
 // 16q .. 16q+15 of each step, q = l >> 4.  Outputs: lane l holds tokens 4q + j (j = 0..3) of row
@@ -40,6 +40,15 @@ typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 #ifndef KQ_GEMV_MFMA_Q6_PLANES
 #define KQ_GEMV_MFMA_Q6_PLANES 0   // 1: Q6_K through the two-plane form instead of sub-block phases
+#endif
+#ifndef KQ_GEMV_MFMA_Q4_PH_MAX
+#define KQ_GEMV_MFMA_Q4_PH_MAX 4   // Q4_K through the phase form up to this many tokens (at most 8)
+#endif
+#ifndef KQ_Q4P_FP1
+#define KQ_Q4P_FP1 4   // super-blocks in flight per wave, Q4_K phase form, 1-4 tokens
+#endif
+#ifndef KQ_Q4P_FP2
+#define KQ_Q4P_FP2 2   // the same, 5-8 tokens
 #endif
 #ifndef KQ_Q6P_FP1
 #define KQ_Q6P_FP1 4   // super-blocks in flight per wave, Q6_K phase form, 1-4 tokens
@@ -311,37 +320,36 @@ k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     }
 }
 
-// ------------------------------------------------------------------ Q6_K by sub-block phases
-// Q6_K's scale changes every 16 columns.  Instead of folding it into two weight planes, this form
-// keeps the raw 6-bit codes (0..63) as the MFMA's B operand and separates the sub-blocks on the A
-// side.  K group q (slots 16q .. 16q+15) of step s carries sub-block j(s, q) = 8(q >> 1) + (q & 1)
-// + 2s, so lane q of a weight row reads ql bytes 64h + 16b and 64h + 32 + 16b, qh bytes 32h + 16b
-// and the scales (h = q >> 1, b = q & 1), 52 bytes, and step s takes nibble s >> 1 of ql word s & 1
-// and bit pair s of qh.  A row a = 4t + p (token t of a group of four, phase p) holds token t's
-// activations in K group (p + s) & 3 only, zeros elsewhere, so output row 4t + p of step s is the
-// 16-element sum S of sub-block j(s, (p + s) & 3) alone, and every A lane carries data in exactly
+// ------------------------------------------------------------------ the phase form (no planes)
+// Instead of folding the sub-block scales into two weight planes, this form keeps the raw codes
+// (Q4_K 0..15, Q6_K 0..63) as the MFMA's B operand and separates 16-element sub-block pieces on the
+// A side.  A row a = 4t + p (token t of a group of four, phase p) holds token t's activations in
+// K group (p + s) & 3 of step s only and zeros in the other three, so output row 4t + p of a
+// K = 64 step is the sum over one 16-element piece alone, and every A lane carries data in exactly
 // one step (its 16 bytes are loaded once and selected per step).  Lane l (q = l >> 4) then holds,
-// for weight row l & 15 and token 4 gi + q, the sums of the step's four sub-blocks, and forms
-//   I = sum_j sc_j * S_j - 32 * sum_j sc_j * b_j
-// (b_j = the Q8_K bsums, sc_j the signed scales): the first sum with 24-bit multiply-adds
-// (|S_j| <= 16 * 128 * 63 < 2^23), the second with one v_mfma_f32_16x16x16_f16 whose operands and
-// partial sums are exact small integers (|b_j| <= 2032, |sc_j| <= 128, |sum| < 2^23).  I is the
-// GEMV's integer, so the per-super-block value and every row are bit-identical to the one-token
-// GEMV; the unpack is ~3.3 VALU per 4 codes instead of ~13 for the planes, and the smaller
-// operands let all four super-blocks of a wave be in flight at once.
+// for weight row l & 15 and token 4 gi + q, the four piece sums of each step and applies the
+// scales with 24-bit multiply-adds (|piece sum| <= 16 * 128 * 63 < 2^23):
+//   Q4_K  K group q of step s = elements 64q + 16s .. +15 (nibble s >> 1 of qs bytes
+//         32q + 16(s & 1) + i: the lane's 32 qs bytes, as in the plane form), sub-block 2q + (s >> 1);
+//         I1 = sum sc_j * S_j, and I2 from the same exact fp16 MFMA as the plane form.
+//   Q6_K  K group q of step s = sub-block j(s, q) = 8(q >> 1) + (q & 1) + 2s: lane q reads ql bytes
+//         64h + 16b and 64h + 32 + 16b, qh bytes 32h + 16b and the scales (h = q >> 1, b = q & 1),
+//         52 bytes, step s taking nibble s >> 1 of ql word s & 1 and bit pair s of qh;
+//         I = sum_j sc_j * S_j - 32 * sum_j sc_j * b_j, the second sum one v_mfma_f32_16x16x16_f16
+//         over the Q8_K bsums b_j and the scales (exact small integers: |b_j| <= 2032,
+//         |sc_j| <= 128, every partial sum < 2^23).
+// The integers are the GEMV's, so the per-super-block values and every row are bit-identical to
+// the one-token GEMV.  The unpack is 1.5 (Q4_K) / ~3.3 (Q6_K) VALU per 4 codes instead of ~3.5 /
+// ~13 for the planes, and the operands are small enough for all four super-blocks of a wave to be
+// in flight at once.  Zero A lanes and the b / B operands of lanes that carry none come from buffer
+// loads past the end of the activation buffer, which return zeros.
 constexpr int MV_OOB = 0x40000000;   // buffer offset beyond any activation buffer: the load returns 0
 
 __device__ __forceinline__ constexpr int q6p_sub(int s, int q) { return 8 * (q >> 1) + (q & 1) + 2 * s; }
 
-// Raw words of one super-block for lane q: ql bytes 64h + 16b and 64h + 32 + 16b, qh bytes
+// Raw Q6_K words of one super-block for lane q: ql bytes 64h + 16b and 64h + 32 + 16b, qh bytes
 // 128 + 32h + 16b, scales, each 16-byte field with the dword after it (funnel-shifted by sh).
 struct MvW6 { u32x4 ql[2], qh, sc; uint32_t qle[2], qhe, sce, sh; };
-
-template <int NG> struct MvX6 {
-    u32x4 a[NG];      // token 4 gi + (l & 15) / 4, sub-block j((q - p) & 3, q): its one active step
-    u32x2 bs[NG];     // bsums 4q .. 4q+3 of token 4 gi + (l & 15) / 4 where l & 3 == 0; else 0
-    float dx[NG];     // d of token 4 gi + q
-};
 
 // The last word read (bytes 208..211 from the aligned base) passes the block end by 2 bytes only
 // for blocks starting at 0 (mod 4), which are never row 7 of a tile column.
@@ -360,8 +368,77 @@ __device__ __forceinline__ void mv6_load(MvW6& w, const uint8_t* bk, int q) {
     w.sce = ld4(b4 + 208);
 }
 
+template <int TYPE> struct MvPh;
+template <> struct MvPh<TYPE_Q4_K> {
+    typedef MvW<TYPE_Q4_K> W;
+    typedef u32x4 B;   // bsums 8(q & 1) .. +7 (the min term's sub-blocks 4(q & 1) .. +3)
+    static __device__ __forceinline__ int a_off(int q, int p) { return 4 + 64 * q + 16 * ((q - p) & 3); }
+    static __device__ __forceinline__ int b_off(int q) { return 260 + 16 * (q & 1); }
+    static __device__ __forceinline__ void load(W& w, const uint8_t* bk, int q) { mv_load(w, bk, q); }
+};
+template <> struct MvPh<TYPE_Q6_K> {
+    typedef MvW6 W;
+    typedef u32x2 B;   // bsums 4q .. 4q+3
+    static __device__ __forceinline__ int a_off(int q, int p) { return 4 + 16 * q6p_sub((q - p) & 3, q); }
+    static __device__ __forceinline__ int b_off(int q) { return 260 + 8 * q; }
+    static __device__ __forceinline__ void load(W& w, const uint8_t* bk, int q) { mv6_load(w, bk, q); }
+};
+
+template <int TYPE, int NG> struct MvXp {
+    u32x4 a[NG];                      // token 4 gi + (l & 15) / 4, the piece of its active step
+    typename MvPh<TYPE>::B bs[NG];    // bsums of token 4 gi + (l & 15) / 4 where l & 3 == 0; else 0
+    float dx[NG];                     // d of token 4 gi + q
+};
+
+__device__ __forceinline__ v4i byte_pieces(const u32x4& v, int shift) {
+    return v4i{(int)((v.x >> shift) & 0x0f0f0f0fu), (int)((v.y >> shift) & 0x0f0f0f0fu),
+               (int)((v.z >> shift) & 0x0f0f0f0fu), (int)((v.w >> shift) & 0x0f0f0f0fu)};
+}
+
 template <int NG>
-__device__ __forceinline__ void mv6_values(const MvW6& w, const MvX6<NG>& x, int q, int p, float (&v)[NG]) {
+__device__ __forceinline__ void mvp_values(const MvW<TYPE_Q4_K>& w, const MvXp<TYPE_Q4_K, NG>& x, int q, int p,
+                                           float (&v)[NG]) {
+    const uint32_t s0 = w.hdr.y, s1 = w.hdr.z, s2 = w.hdr.w;
+    // the eight 6-bit scales (bytes of sca: sub-blocks 0..3, of scb: 4..7) and mins (q4kernels.h:17-18)
+    const uint32_t sca = s0 & 0x3f3f3f3fu, scb = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t ma = s1 & 0x3f3f3f3fu, mb = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+    const v4i bq[4] = {byte_pieces(w.qa, 0), byte_pieces(w.qb, 0), byte_pieces(w.qa, 4), byte_pieces(w.qb, 4)};
+    // min term, as the plane form: K slots 4q .. 4q+3 = sub-blocks 4(q & 1) .. +3, the high (q < 2) or
+    // low part of B against -64 m or -m
+    const uint32_t mw = (q & 1) ? mb : ma;
+    const float f = (q >> 1) ? -1.0f : -64.0f;
+    const v4h bm = __builtin_bit_cast(v4h, u32x2{mv_pk_f16(f * (float)byte_of(mw, 0), f * (float)byte_of(mw, 1)),
+                                                 mv_pk_f16(f * (float)byte_of(mw, 2), f * (float)byte_of(mw, 3))});
+    const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) {
+        const v4i xa = __builtin_bit_cast(v4i, x.a[gi]);
+        int I1 = 0;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const v4i a = ((p + s) & 3) == q ? xa : zero;
+            const v4i S = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq[s], zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {          // output row 4q + r: K group (r + s) & 3, sub-block 2k + (s >> 1)
+                const int j = 2 * ((r + s) & 3) + (s >> 1);
+                I1 += (int)byte_of(j < 4 ? sca : scb, j & 3) * ((S[r] << 8) >> 8);   // 24-bit operands
+            }
+        }
+        const uint32_t bw[4] = {x.bs[gi].x, x.bs[gi].y, x.bs[gi].z, x.bs[gi].w};
+        float B[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int sb = shalf(bw[k], 0) + shalf(bw[k], 1);
+            B[k] = (float)((q >> 1) ? (sb & 63) : (sb >> 6));
+        }
+        const v4h am = __builtin_bit_cast(v4h, u32x2{mv_pk_f16(B[0], B[1]), mv_pk_f16(B[2], B[3])});
+        const v4f cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);   // -I2
+        v[gi] = q4k_value(w.hdr.x, x.dx[gi], I1, (int)(-cm[0]));
+    }
+}
+
+template <int NG>
+__device__ __forceinline__ void mvp_values(const MvW6& w, const MvXp<TYPE_Q6_K, NG>& x, int q, int p, float (&v)[NG]) {
     const uint32_t sh = w.sh;
     const u32x4 QL[2] = {mv_funnel(w.ql[0], w.qle[0], sh), mv_funnel(w.ql[1], w.qle[1], sh)};
     const u32x4 QH = mv_funnel(w.qh, w.qhe, sh);
@@ -410,12 +487,21 @@ __device__ __forceinline__ void mv6_values(const MvW6& w, const MvX6<NG>& x, int
     }
 }
 
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ void buf_ld(u32x4& v, __amdgpu_buffer_rsrc_t r, int off) { v = buf_ld16(r, off); }
+__device__ __forceinline__ void buf_ld(u32x2& v, __amdgpu_buffer_rsrc_t r, int off) {
+    v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+
 // Workgroup and merge as k_gemv_mfma; NG groups of four tokens (N <= 4 NG) share each unpack; FP of
 // the wave's four super-blocks are in flight before the first is used.
-template <int NG, int LB, int FP>
+template <int TYPE, int NG, int LB, int FP>
 __global__ void __launch_bounds__(LB)
-k_gemv_mfma_q6(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
-    constexpr int BS = Q6K_BYTES;
+k_gemv_mfma_ph(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
+    typedef MvPh<TYPE> Ph;
+    constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float part[16][16][MV_ROWS];            // [chunk][token][row] chunk sums
     const int lane = threadIdx.x & 63;
     const int chunk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -433,40 +519,39 @@ k_gemv_mfma_q6(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     const int xrow = G * Q8K_BYTES;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(XQ), 0, N * xrow, 0x00020000);
     const int t = l16 >> 2, p = lane & 3;
-    const int ja = q6p_sub((q - p) & 3, q);            // the sub-block of this lane's active step
     int aoff[NG], boff[NG];
     const uint8_t* xd[NG];
 #pragma unroll
     for (int gi = 0; gi < NG; gi++) {
         const int tok = 4 * gi + t;
-        aoff[gi] = tok < N ? tok * xrow + 4 + 16 * ja : MV_OOB;
-        boff[gi] = p == 0 && tok < N ? tok * xrow + 260 + 8 * q : MV_OOB;
+        aoff[gi] = tok < N ? tok * xrow + Ph::a_off(q, p) : MV_OOB;
+        boff[gi] = p == 0 && tok < N ? tok * xrow + Ph::b_off(q) : MV_OOB;
         const int n = 4 * gi + q;
         xd[gi] = XQ + (int64_t)(n < N ? n : N - 1) * xrow;
     }
 
     const int g0 = MV_CHUNK * chunk;
-    auto load = [&](int s, MvW6& ww, MvX6<NG>& xx) {
+    auto load = [&](int s, typename Ph::W& ww, MvXp<TYPE, NG>& xx) {
         const int g = g0 + s < G ? g0 + s : G - 1;
-        mv6_load(ww, wrow + (int64_t)g * col_bytes, q);
+        Ph::load(ww, wrow + (int64_t)g * col_bytes, q);
         const int go = g * Q8K_BYTES;
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
-            xx.a[gi] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff[gi] + go, 0, 0));
-            xx.bs[gi] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(xr, boff[gi] + go, 0, 0));
+            xx.a[gi] = buf_ld16(xr, aoff[gi] + go);
+            buf_ld(xx.bs[gi], xr, boff[gi] + go);
             xx.dx[gi] = __builtin_bit_cast(float, ld4(xd[gi] + go));
         }
     };
     float v[MV_CHUNK][NG];
-    MvW6 w[FP];
-    MvX6<NG> x[FP];
+    typename Ph::W w[FP];
+    MvXp<TYPE, NG> x[FP];
 #pragma unroll
     for (int s = 0; s < FP; s++) load(s, w[s], x[s]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < MV_CHUNK; s++) {
         float vv[NG];
-        mv6_values<NG>(w[s % FP], x[s % FP], q, p, vv);
+        mvp_values<NG>(w[s % FP], x[s % FP], q, p, vv);
         const bool valid = g0 + s < G;          // columns past G contribute +0
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) v[s][gi] = valid ? vv[gi] : 0.0f;
@@ -503,14 +588,17 @@ static void launch_mv(const MvGroup& mg, int wgs, const uint8_t* xq, int N, int 
                        N, G);
 }
 
-// n (1..3) matrices of one type, N = 2..16 tokens, C <= 16384 (at most 16 chunks of 4 columns).
+// n (1..3) matrices of one type, N = 1..16 tokens, C <= 16384 (at most 16 chunks of 4 columns).
 // Schedules by shape, each the fastest measured for its case (12288x4096 and 4096x12288 Q4_K,
 // 4096x12288 and 1024x4096 Q6_K; N = 3..16):
-//   Q4_K, G <= 16: all four super-blocks in flight (3 waves per SIMD);
-//   Q4_K, G > 16 and Q6_K beyond 8 tokens or 48 super-blocks: two in flight, behind the barrier;
+//   Q4_K up to 4 tokens and 48 super-blocks: the phase form, all four super-blocks in flight
+//   (12288x4096 at N = 2 / 4: plane form 10.2 / 10.0 -> 8.0 / 8.2 us; at 5..8 tokens the plane form
+//   stays faster, 9.9 / 10.6 against 10.3 / 10.8 us);
 //   Q6_K up to 8 tokens and 48 super-blocks: the phase form, all four super-blocks in flight for
 //   up to 4 tokens, two for 5..8 (4096x12288 at N = 3 / 4 / 5 / 8: 15.3 / 15.3 / 15.3 / 16.1 ->
-//   12.7 / 12.8 / 14.0 / 14.4 us; 4096x4096 at N = 4: 7.0 -> 5.9 us).
+//   12.7 / 12.8 / 14.0 / 14.4 us; 4096x4096 at N = 4: 7.0 -> 5.9 us);
+//   otherwise the plane form: Q4_K with G <= 16 all four super-blocks in flight (3 waves per SIMD),
+//   else two in flight, behind the barrier.
 void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
                             int N, float* const* y, const int64_t* ldy, hipStream_t s) {
     const int G = C / QK;
@@ -525,19 +613,24 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
         wgs += (R[i] + MV_ROWS - 1) / MV_ROWS;
     }
     for (int i = n; i < 4; i++) mg.first[i] = wgs;
-    if (type == TYPE_Q4_K) {
+    const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
+    const dim3 grid(wgs), block(64 * nchunks);
+    // the phase form up to 8 tokens and 48 super-blocks: beyond 8 tokens (three or four token groups)
+    // it needs more registers than 3 waves per SIMD leave and spills, beyond 48 super-blocks a
+    // workgroup has 16 waves, 4 per SIMD (128 registers: spills too)
+    const bool ph = G <= 48 && N <= 8 && (type == TYPE_Q4_K ? N <= KQ_GEMV_MFMA_Q4_PH_MAX : !KQ_GEMV_MFMA_Q6_PLANES);
+    if (ph && type == TYPE_Q4_K) {
+        if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q4_K, 1, 768, KQ_Q4P_FP1>), grid, block, 0, s, mg, xq, N, G);
+        else hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q4_K, 2, 768, KQ_Q4P_FP2>), grid, block, 0, s, mg, xq, N, G);
+    } else if (ph) {
+        if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q6_K, 1, 768, KQ_Q6P_FP1>), grid, block, 0, s, mg, xq, N, G);
+        else hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q6_K, 2, 768, KQ_Q6P_FP2>), grid, block, 0, s, mg, xq, N, G);
+    } else if (type == TYPE_Q4_K) {
         if (G <= 16) launch_mv<TYPE_Q4_K, 256, true, true>(mg, wgs, xq, N, G, s);
         else if (G <= 48) launch_mv<TYPE_Q4_K, 768, false, true>(mg, wgs, xq, N, G, s);
         else launch_mv<TYPE_Q4_K, 1024, false, true>(mg, wgs, xq, N, G, s);
-    } else if (KQ_GEMV_MFMA_Q6_PLANES || N > 8 || G > 48) {
-        // beyond 8 tokens the phase form needs more registers than 3 waves per SIMD leave (spills);
-        // beyond 48 super-blocks a workgroup has 16 waves, 4 per SIMD (128 registers: spills too)
-        launch_mv<TYPE_Q6_K, 1024, false, true>(mg, wgs, xq, N, G, s);
     } else {
-        const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
-        const dim3 grid(wgs), block(64 * nchunks);
-        if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_q6<1, 768, KQ_Q6P_FP1>), grid, block, 0, s, mg, xq, N, G);
-        else hipLaunchKernelGGL((k_gemv_mfma_q6<2, 768, KQ_Q6P_FP2>), grid, block, 0, s, mg, xq, N, G);
+        launch_mv<TYPE_Q6_K, 1024, false, true>(mg, wgs, xq, N, G, s);
     }
 }
 

@@ -43,19 +43,6 @@
 #ifndef KQ_GEMV_SEQ_WPB
 #define KQ_GEMV_SEQ_WPB 4        // waves per workgroup of the sequential kernel
 #endif
-#ifndef KQ_GEMV_MFMA_MIN_N
-#define KQ_GEMV_MFMA_MIN_N 3     // tokens per call from which the MFMA form (gemv_mfma.hip) is used
-#endif
-#ifndef KQ_GEMV_MFMA_MIN_N_Q4_WIDE
-#define KQ_GEMV_MFMA_MIN_N_Q4_WIDE 2   // the same for Q4_K with C > 4096
-#endif
-// The MFMA form runs one workgroup per 16 rows; below this many rows in a call (fewer than 256
-// workgroups) it leaves CUs idle, and up to 4 tokens the v_dot4 kernels are faster there (N = 3 / 4:
-// 1024x4096 Q6_K 6.8 / 6.9 -> 4.7 / 5.5 us, 2048x12288 Q6_K 13.9 / 14.1 -> 10.9 / 12.7 us, 1024x4096
-// Q4_K 5.2 / 5.3 -> 4.3 / 5.1 us; from 4096 rows the MFMA form is as fast or faster at N = 4).
-#ifndef KQ_GEMV_MFMA_MIN_ROWS
-#define KQ_GEMV_MFMA_MIN_ROWS 4096
-#endif
 #ifndef KQ_GEMV_SPLIT_MAX
 #define KQ_GEMV_SPLIT_MAX 4      // most column passes handled by the pass-split kernel (Q4_K)
 #endif
@@ -810,17 +797,38 @@ static void launch1(const MatGroup& mg, const uint8_t* xq, int G, int nt, int rp
     }
 }
 
+// Whether a call goes to the MFMA forms (gemv_mfma.hip, at most 64 super-blocks per row) rather than
+// the v_dot4 kernels here; every choice is the faster one measured (us, v_dot4 -> MFMA form):
+//   Q4_K  one token with 17..48 super-blocks per row and at least 4096 rows (the phase form against the
+//         pass-split kernel): 4096x12288 9.2 -> 8.6; below 4096 rows the v_dot4 kernel stays (2048x12288
+//         6.2 against ~6.7).  2..4 tokens: the phase form, 12288x4096 at N = 2 9.4 -> 8.0, 4096x12288
+//         10.4 -> 8.4, 2048x12288 at N = 2 / 3 / 4 7.8 / 9.0 / 11.0 -> 6.7 / 6.7 / 6.7; except below
+//         4096 rows with at most 16 super-blocks and at most 3 tokens (1024x4096 at N = 2 3.8 against
+//         4.4, N = 3 4.3 against 4.4), and below 4096 rows with more than 48 (not measured with the
+//         phase form, which stops at 48).  5..16 tokens: the plane form.
+//   Q6_K  from 3 tokens (2 tokens: 12.1 against 13.7); below 4096 rows from 5 tokens (N = 3 / 4: 1024x4096
+//         4.7 / 5.5 against 5.7 / 5.7, 2048x12288 10.8 / 12.6 against 11.4 / 11.6).
+static bool use_mfma_form(int type, int N, int G, int rows) {
+    if (G > 64) return false;
+    const bool few_rows = rows < 4096;
+    if (type == TYPE_Q4_K) {
+        if (N == 1) return G > 16 && G <= 48 && !few_rows;
+        if (few_rows && N <= 4 && (G > 48 || (G <= 16 && N <= 3))) return false;
+        return true;
+    }
+    return N >= 3 && !(few_rows && N <= 4);
+}
+
 // n matrices of one type sharing xq (N tokens); tokens go in groups of up to 4 per launch, each
 // group an independent launch over the same weights.  first_unit[] is filled with row-tile
 // prefix counts here and scaled to units per RPW in launch3.
 void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, int type,
                            const uint8_t* xq, int N, float* const* y, const int64_t* ldy, hipStream_t s) {
     const int G = C / QK;
-    const int mfma_min = type == TYPE_Q4_K && G > 16 ? KQ_GEMV_MFMA_MIN_N_Q4_WIDE : KQ_GEMV_MFMA_MIN_N;
     int rows = 0;
     for (int i = 0; i < n; i++) rows += R[i];
-    const bool few_rows = N <= 4 && rows < KQ_GEMV_MFMA_MIN_ROWS;
-    if (N >= mfma_min && G <= 64 && !few_rows) {   // the MFMA form (same bits)
+    if (use_mfma_form(type, N, G, rows)) {   // same bits
+
         launch_gemv_mfma_group(n, w, R, C, type, xq, N, y, ldy, s);
         return;
     }

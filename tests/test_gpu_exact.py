@@ -106,9 +106,10 @@ def test_gemm_exact(dev, orc, ty, R, C, M, amp):
                                         (12, 1024, 12288, 1), (14, 1024, 12288, 1), (12, 64, 16640, 1),
                                         (14, 40, 16640, 1)])
 def test_gemv_batches_exact(dev, orc, ty, R, C, amp):
-    """N = 1, 2 (v_dot4 GEMV; Q4_K with 4096 < C <= 16384 and at least 4096 rows takes the MFMA
-    planes from N = 2), N = 3, 4 (MFMA planes from 4096 rows, v_dot4 below) and N = 8, 16 (MFMA
-    planes; beyond 16384 columns the v_dot4 kernel again): every row exact."""
+    """Every kernel choice of kq_gemv_q8k: the v_dot4 GEMVs (N = 1, 2 and few rows), the phase form
+    of the MFMA kernel (Q4_K: N = 2..4, and N = 1 with 4096 < C <= 12288 and at least 4096 rows;
+    Q6_K: N = 3..8 from 4096 rows), the plane form (N = 16; Q4_K N = 8) and, beyond 16384 columns,
+    the v_dot4 kernel again: every row exact."""
     print("gemv exact", ty, R, C, flush=True)
     W, X, xq, ref = prepare(orc, R, C, ty, 16, seed=R + C + 7, amp=amp)
     wd, xqd = dev_t(W, dev), dev_t(xq, dev)

@@ -801,8 +801,10 @@ static void launch1(const MatGroup& mg, const uint8_t* xq, int G, int nt, int rp
 // the v_dot4 kernels here; every choice is the faster one measured (us, v_dot4 -> MFMA form):
 //   Q4_K  one token with 17..48 super-blocks per row and at least 4096 rows (the phase form against the
 //         pass-split kernel): 4096x12288 9.2 -> 8.6; below 4096 rows the v_dot4 kernel stays (2048x12288
-//         6.2 against ~6.7).  2..4 tokens: the phase form, 12288x4096 at N = 2 9.4 -> 8.0, 4096x12288
-//         10.4 -> 8.4, 2048x12288 at N = 2 / 3 / 4 7.8 / 9.0 / 11.0 -> 6.7 / 6.7 / 6.7; except below
+//         6.2 against ~6.7), and so does every one-token call with at most 16 (6144 / 4096 / 12288 /
+//         24576 x 4096: 5.2 / 4.5 / 8.3 / 12.7 against 5.7 / 4.7 / 8.4 / 12.7).  2..4 tokens: the phase
+//         form, 12288x4096 at N = 2 9.4 -> 8.0, 4096x12288 10.4 -> 8.4, 2048x12288 at N = 2 / 3 / 4
+//         7.8 / 9.0 / 11.0 -> 6.7 / 6.7 / 6.7; except below
 //         4096 rows with at most 16 super-blocks and at most 3 tokens (1024x4096 at N = 2 3.8 against
 //         4.4, N = 3 4.3 against 4.4), and below 4096 rows with more than 48 (not measured with the
 //         phase form, which stops at 48).  5..16 tokens: the plane form.

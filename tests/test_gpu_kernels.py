@@ -168,6 +168,7 @@ def test_gemv_q8k_reference_inputs(dev, orc, ty):
     (14, 8, 256), (12, 24, 16384), (14, 40, 16640),         # half row tile, one column; G = 64; G = 65
     (14, 4088, 4096), (12, 4096, 12288),                    # either side of the 4096-row MFMA threshold
     (12, 1000, 4096),                                       # Q4_K below it: v_dot4 to 3 tokens, then MFMA
+    (12, 4096, 8448), (14, 4096, 12032),                    # G = 33 / 47: a last chunk of 1 / 3 super-blocks
 ])
 def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
     """Speculative-verify invariant: every row of a batch equals its N = 1 result bit for bit."""

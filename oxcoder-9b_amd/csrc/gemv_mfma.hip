@@ -517,6 +517,8 @@ k_gemv_mfma_ph(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     const int64_t col_bytes = 8 * BS;
     const uint8_t* wrow = mg.w[m] + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
     const int xrow = G * Q8K_BYTES;
+    // raw buffer over the N activation rows: stride 0, N * xrow bytes (loads past them return 0), and
+    // the gfx9 descriptor word 3 (32-bit data format)
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(XQ), 0, N * xrow, 0x00020000);
     const int t = l16 >> 2, p = lane & 3;
     int aoff[NG], boff[NG];

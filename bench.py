@@ -13,7 +13,7 @@ value = algorithmic bytes per step (weights + activations read + outputs written
         / measured time per step, in GB/s.
 Also reported: the dominant kernel's roofline fraction (Q4_K GEMV, per-launch HIP events), the
 reference CPU path (kc_matvec, fp32 activations) on the host cores, speculative-verify batched
-GEMV, the fp32-activation drop-in over the same layer, the prefill GEMM, the output heads and the
+GEMV (per matrix and through the layer), the fp32-activation drop-in over the same layer, the prefill GEMM, the output heads and the
 full decode weight stream.
 """
 import argparse
@@ -64,22 +64,22 @@ class Runner:
     def stream(self):
         return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
 
-    def quantize(self, x, C_, xq, s):
-        self.check(self.lib.kq_q8k_quantize(C.c_void_p(x.data_ptr()), C_, C_, 1, C.c_void_p(xq.data_ptr()), s))
+    def quantize(self, x, C_, xq, s, N=1):
+        self.check(self.lib.kq_q8k_quantize(C.c_void_p(x.data_ptr()), C_, C_, N, C.c_void_p(xq.data_ptr()), s))
 
     def gemv(self, w, R, C_, ty, xq, N, y, s):
         self.check(self.lib.kq_gemv_q8k(C.c_void_p(w.data_ptr()), R, C_, ty, C.c_void_p(xq.data_ptr()), N,
                                         C.c_void_p(y.data_ptr()), R, s))
 
-    def gemv_multi(self, mats, xq, ys, s):
-        """mats: [(w, R, C, type)] sharing xq (one token); one launch per type."""
+    def gemv_multi(self, mats, xq, ys, s, N=1):
+        """mats: [(w, R, C, type)] sharing xq (N tokens; y rows of R floats); one launch per type."""
         n = len(mats)
         W = (C.c_void_p * n)(*[m[0].data_ptr() for m in mats])
         Rs = (C.c_int * n)(*[m[1] for m in mats])
         Ts = (C.c_int * n)(*[m[3] for m in mats])
         Y = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
         L = (C.c_int64 * n)(*[m[1] for m in mats])
-        self.check(self.lib.kq_gemv_q8k_multi(n, W, Rs, mats[0][2], Ts, C.c_void_p(xq.data_ptr()), 1, Y, L, s))
+        self.check(self.lib.kq_gemv_q8k_multi(n, W, Rs, mats[0][2], Ts, C.c_void_p(xq.data_ptr()), N, Y, L, s))
 
     def rms_q8k(self, h, res, w, D, xq, s):
         """kq_rms_q8k on one row: h += res, xq = Q8_K(RMSNorm(h) * w)."""
@@ -348,6 +348,37 @@ def batched_extra(torch, rn, dev, steps):
             nbytes = wbytes(R, C_, ty) + N * (C_ // 256) * Q8K + N * R * 4
             out["%s_N%d" % (name, N)] = {"us": round(per * 1e6, 2), "GB/s": round(nbytes / per / 1e9, 1),
                                          "TOPS": round(2 * N * R * C_ / per / 1e12, 2)}
+    return out
+
+
+def verify_layer_extra(torch, rn, layers, dev, steps=320):
+    """Speculative verify of N draft tokens through one decode layer's 7 matrices (the batched form of
+    the step: Engine.gemv_batch's path; the ternary engine's spec.verify, spec.py:790): each of the 4
+    inputs quantized as N Q8_K rows, the matrices sharing it in one kq_gemv_q8k_multi call with N
+    tokens, every row bit-identical to one token.  N = 1 is the decode step itself; vs_one_token is
+    what verifying N tokens costs against decoding one."""
+    from kq import quantize as kqq
+    out = {}
+    reps = max(1, steps // len(layers))
+    for N in (1, 2, 4, 8):
+        xs = [torch.from_numpy(kqq.synthetic_activations(N, c, seed=20 + i)).to(dev) for i, c in enumerate(INPUT_COLS)]
+        xqs = [torch.empty(N * (c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
+        ys = {name: torch.empty((N, R), device=dev) for name, R, _, _, _ in LAYER}
+
+        def run():
+            s = rn.stream()
+            for lay in layers:
+                for slot, C_ in enumerate(INPUT_COLS):
+                    rn.quantize(xs[slot], C_, xqs[slot], s, N)
+                    group = [(n, R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == slot]
+                    rn.gemv_multi([(lay[n], R, C2, ty) for n, R, C2, ty in group], xqs[slot],
+                                  [ys[n] for n, *_ in group], s, N)
+        g = capture(torch, run)
+        time_graphs(torch, [g] * 2)
+        per = time_graphs(torch, [g] * reps) / (reps * len(layers))
+        out["N%d_us" % N] = round(per * 1e6, 2)
+    for N in (2, 4, 8):
+        out["N%d_vs_one_token" % N] = round(out["N%d_us" % N] / out["N1_us"], 3)
     return out
 
 
@@ -762,8 +793,8 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
-    ap.add_argument("--only", choices=("batched", "producers", "f32_layer", "gemm", "head", "decode_stream", "pack",
-                                       "tp_shard", "prefill_chunk"),
+    ap.add_argument("--only", choices=("batched", "verify", "producers", "f32_layer", "gemm", "head", "decode_stream",
+                                       "pack", "tp_shard", "prefill_chunk"),
                     help="run only this extra (no headline step, no CPU baseline) and print its JSON; for "
                          "profiling one workload")
     ap.add_argument("--pmc-workload", choices=("gemv", "gemm", "q6k"),
@@ -790,9 +821,10 @@ def main():
         pmc_workload_q6k(torch, rn, dev)
         return
     if a.only:
-        need_layers = a.only in ("producers", "f32_layer", "prefill_chunk")
+        need_layers = a.only in ("verify", "producers", "f32_layer", "prefill_chunk")
         lay = make_layer(torch, dev, a.copies) if need_layers else None
         fn = {"batched": lambda: batched_extra(torch, rn, dev, 160),
+              "verify": lambda: verify_layer_extra(torch, rn, lay, dev),
               "producers": lambda: producers_extra(torch, rn, lay, dev),
               "f32_layer": lambda: f32_layer_extra(torch, rn, lay, dev),
               "gemm": lambda: gemm_extra(torch, rn, dev),
@@ -865,6 +897,8 @@ def main():
     if not a.no_extras:
         log("bench: batched GEMV")
         result["batched_gemv"] = batched_extra(torch, rn, dev, 160)
+        log("bench: speculative verify through a layer")
+        result["verify_layer"] = verify_layer_extra(torch, rn, layers, dev)
         log("bench: fused producers")
         result["producers"] = producers_extra(torch, rn, layers, dev)
         log("bench: fp32-activation layer")

@@ -17,9 +17,9 @@
 // and [-64 m_s, -m_s], which returns -I2 exactly.  Up to 4 (Q4_K) or 8 (Q6_K) tokens a second form
 // is used (k_gemv_mfma_ph, below): raw codes against sub-block-phased activations, no planes.
 //
-// MFMA lanes: lane l serves token (A operand) and weight row (B operand) l & 15 and K slots
-// 16q .. 16q+15 of each step, q = l >> 4.  Outputs: lane l holds tokens 4q + j (j = 0..3) of row
-// l & 15.  Which super-block elements a K slot carries is free (the products are exact integer
+// MFMA lanes (the plane form): lane l serves token (A operand) and weight row (B operand) l & 15 and K slots
+// 16q .. 16q+15 of each step, q = l >> 4.  Outputs: lane l holds tokens 4q + j (j = 0..3) of
+// row l & 15.  Which super-block elements a K slot carries is free (the products are exact integer
 // sums), so each type uses the assignment that loads its bytes best:
 //   Q4_K: lane q reads qs bytes 32q .. 32q+31 (sub-blocks 2q and 2q+1, the GEMV's lane layout),
 //         each quant byte once per row; step p takes bytes 32q + 8p .. +7, low nibbles (elements

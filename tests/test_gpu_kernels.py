@@ -187,6 +187,35 @@ def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
     assert_close_inf(s, orc.gemv_q8k(host(W), R, C, ty, xq, 16))
 
 
+def test_small_batch_forms_sweep(dev, orc):
+    """Every small-batch kernel choice over seeded shapes: super-blocks per row G = 1, 2, 3, 5, 16, 17,
+    33, 47, 48 (whole and partial chunks of 4), rows below, at and above 4096 and not a multiple of 16,
+    N = 2..8 (the phase form of the MFMA kernel, the v_dot4 kernels for few rows, the plane form
+    beyond): each row bit-identical to its one-token result and the batch within the bar of the
+    oracle.  The oracle runs on every fourth case (it is the slow part)."""
+    cases = [(12, 4104, 256), (14, 4104, 256), (12, 4096, 512), (14, 4112, 768), (12, 4088, 1280),
+             (14, 4096, 1280), (12, 4096, 4352), (14, 4096, 4352), (12, 4104, 8448), (14, 4096, 8448),
+             (12, 4096, 12032), (14, 4104, 12032), (12, 24, 12288), (14, 40, 4096), (12, 8200, 4096),
+             (14, 8200, 4352)]
+    for i, (ty, R, C) in enumerate(cases):
+        print("forms sweep", ty, R, C, flush=True)
+        W = synth(R, C, ty, 500 + i)
+        Wd = dev_t(W, dev)
+        X = kqq.synthetic_activations(8, C, seed=600 + i)
+        xq = orc.quantize_q8k(X)
+        xqd = dev_t(xq, dev)
+        single = torch.empty((8, R), device=dev)
+        for n in range(8):
+            ops.gemv_q8k(Wd, R, C, ty, xqd[n:n + 1], 1, single[n])
+        s = host(single)
+        for N in (2, 3, 4, 5, 6, 7, 8):
+            yb = torch.empty((N, R), device=dev)
+            ops.gemv_q8k(Wd, R, C, ty, xqd, N, yb)
+            np.testing.assert_array_equal(host(yb), s[:N], err_msg="%d %d %d N=%d" % (ty, R, C, N))
+        if i % 4 == 0:
+            assert_close_inf(s, orc.gemv_q8k(W, R, C, ty, xq, 8))
+
+
 @pytest.mark.parametrize("ty", [12, 14])
 def test_batched_reference_inputs_bit_identical(dev, orc, ty):
     """The reference unit test's random block bytes (any scale/min bit pattern) through the

@@ -129,3 +129,41 @@ def test_gemv_f32_exact(dev, orc, ty):
         y = torch.empty(R, device=dev)
         ops.gemv(wd, R, C, ty, dev_t(X[n], dev), y)
         assert_exact(host(y), ref[n], "f32 gemv")
+
+
+@pytest.mark.parametrize("ty", [12, 14])
+def test_small_batch_extreme_blocks(dev, orc, ty):
+    """The integers at their largest: every code at its maximum (Q4_K 15, Q6_K 63) or minimum, scales and
+    mins at their extremes (Q4_K 63, Q6_K -128 / 127), fp16 block scales 1, and activation blocks of
+    +-127 (Q8_K d = 1): per-piece sums near 2^17, products with the scales near 2^24, super-block
+    integers near 2^28.  Rows of every batch size through every kernel choice (v_dot4, the phase and the
+    plane MFMA forms) must equal the one-token rows bit for bit, and the oracle within the bar."""
+    R, C = 4096, 4096
+    G = C // 256
+    rng = np.random.default_rng(5 + ty)
+    if ty == 12:
+        raw = np.zeros((R, G, 144), np.uint8)
+        raw[:, :, 0:2] = ONE_F16
+        raw[:, :, 2:4] = ONE_F16
+        raw[:, :, 4:16] = 0xFF                                      # every 6-bit scale and min 63
+        raw[:, :, 16:] = np.where(rng.random((R, G, 128)) < 0.5, 0xFF, 0x00).astype(np.uint8)
+    else:
+        raw = np.zeros((R, G, 210), np.uint8)
+        raw[:, :, 0:192] = np.where(rng.random((R, G, 192)) < 0.5, 0xFF, 0x00).astype(np.uint8)   # codes 63 or 0
+        raw[:, :, 192:208] = np.where(rng.random((R, G, 16)) < 0.5, 0x80, 0x7F).astype(np.uint8)   # -128 / 127
+        raw[:, :, 208:210] = ONE_F16
+    W = kqq.tile(raw.reshape(-1), R, C, ty)
+    X = np.where(rng.random((16, C)) < 0.5, 127.0, -127.0).astype(np.float32)
+    xq = orc.quantize_q8k(X)
+    wd, xqd = dev_t(W, dev), dev_t(xq, dev)
+    single = torch.empty((16, R), device=dev)
+    for n in range(16):
+        ops.gemv_q8k(wd, R, C, ty, xqd[n:n + 1], 1, single[n])
+    s = host(single)
+    ref = orc.gemv_q8k(W, R, C, ty, xq, 16)
+    err = np.abs(s.astype(np.float64) - ref).max()
+    assert err <= 1e-5 * np.abs(ref).max(), err
+    for N in (2, 3, 4, 5, 8, 16):
+        y = torch.empty((N, R), device=dev)
+        ops.gemv_q8k(wd, R, C, ty, xqd, N, y)
+        np.testing.assert_array_equal(host(y), s[:N], err_msg="N=%d" % N)

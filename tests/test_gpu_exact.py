@@ -167,3 +167,34 @@ def test_small_batch_extreme_blocks(dev, orc, ty):
         y = torch.empty((N, R), device=dev)
         ops.gemv_q8k(wd, R, C, ty, xqd, N, y)
         np.testing.assert_array_equal(host(y), s[:N], err_msg="N=%d" % N)
+
+
+@pytest.mark.parametrize("ty,C", [(12, 4096), (14, 12288)])
+def test_gemm_extreme_blocks(dev, orc, ty, C):
+    """The prefill GEMM (both entry points, K split or not) on the same extreme blocks: codes, scales and
+    mins at their extremes, activations +-127, so every plane and the shifted sweep sums reach their
+    largest magnitudes (Q6_K: 256 * (x.H) near 2^27); within the bar of the oracle."""
+    R, M = 512, 300
+    G = C // 256
+    rng = np.random.default_rng(50 + ty)
+    if ty == 12:
+        raw = np.zeros((R, G, 144), np.uint8)
+        raw[:, :, 0:2] = ONE_F16
+        raw[:, :, 2:4] = ONE_F16
+        raw[:, :, 4:16] = 0xFF
+        raw[:, :, 16:] = np.where(rng.random((R, G, 128)) < 0.5, 0xFF, 0x00).astype(np.uint8)
+    else:
+        raw = np.zeros((R, G, 210), np.uint8)
+        raw[:, :, 0:192] = np.where(rng.random((R, G, 192)) < 0.5, 0xFF, 0x00).astype(np.uint8)
+        raw[:, :, 192:208] = np.where(rng.random((R, G, 16)) < 0.5, 0x80, 0x7F).astype(np.uint8)
+        raw[:, :, 208:210] = ONE_F16
+    W = kqq.tile(raw.reshape(-1), R, C, ty)
+    X = np.where(rng.random((M, C)) < 0.5, 127.0, -127.0).astype(np.float32)
+    xq = orc.quantize_q8k(X)
+    ref = orc.gemv_q8k(W, R, C, ty, xq, M)
+    wd, xqd = dev_t(W, dev), dev_t(xq, dev)
+    for ws in (None, ops.gemm_workspace(R, C, M, dev)):
+        y = torch.empty((M, R), device=dev)
+        ops.gemm_q8k(wd, R, C, ty, xqd, M, y, ws=ws)
+        got = host(y).astype(np.float64)
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()

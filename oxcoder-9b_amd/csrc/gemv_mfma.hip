@@ -217,6 +217,29 @@ __device__ __forceinline__ void mv_values(const MvW<TYPE_Q6_K>& w, const MvX& x,
     for (int j = 0; j < 4; j++) v[j] = q6k_value(d, x.dx[j], acc[j]);
 }
 
+// After the barrier: thread (token n, row r) merges the chunk sums of each 16-column pass as
+// ((c0+c1)+(c2+c3)) (missing chunks +0) and the passes with the pass tree, and stores y.
+__device__ __forceinline__ void mv_merge(const float (*part)[16][MV_ROWS], int nchunks, int G, int N, int R, int row0,
+                                         float* y, int64_t ldy) {
+    const int passes = (G + 15) / 16;
+    for (int idx = threadIdx.x; idx < N * MV_ROWS; idx += blockDim.x) {
+        const int n = idx / MV_ROWS, r = idx - n * MV_ROWS;
+        if (row0 + r >= R) continue;
+        PassTree tr;
+        tree_init(tr);
+        for (int ps = 0; ps < passes; ps++) {
+            float c[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int cc = 4 * ps + k;
+                c[k] = cc < nchunks ? part[cc][n][r] : 0.0f;
+            }
+            tree_push(tr, __fadd_rn(__fadd_rn(c[0], c[1]), __fadd_rn(c[2], c[3])));
+        }
+        y[(int64_t)n * ldy + row0 + r] = tree_final(tr);
+    }
+}
+
 // ------------------------------------------------------------------ the kernel
 // Workgroup: 16 rows of one matrix, one wave per chunk of 4 super-blocks (ceil(G/4) <= 16 waves).
 // Load schedule of a wave's chunk: with PRE_ALL every super-block's loads are issued before the
@@ -301,23 +324,7 @@ k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     __syncthreads();
 
     // merge: thread (token n, row r); passes of 4 chunks, missing chunks are +0
-    const int passes = (G + 15) / 16;
-    for (int idx = threadIdx.x; idx < N * MV_ROWS; idx += blockDim.x) {
-        const int n = idx / MV_ROWS, r = idx - n * MV_ROWS;
-        if (row0 + r >= R) continue;
-        PassTree tr;
-        tree_init(tr);
-        for (int ps = 0; ps < passes; ps++) {
-            float c[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int cc = 4 * ps + k;
-                c[k] = cc < nchunks ? part[cc][n][r] : 0.0f;
-            }
-            tree_push(tr, __fadd_rn(__fadd_rn(c[0], c[1]), __fadd_rn(c[2], c[3])));
-        }
-        mg.y[m][(int64_t)n * mg.ldy[m] + row0 + r] = tree_final(tr);
-    }
+    mv_merge(part, nchunks, G, N, R, row0, mg.y[m], mg.ldy[m]);
 }
 
 // ------------------------------------------------------------------ the phase form (no planes)
@@ -564,23 +571,7 @@ k_gemv_mfma_ph(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
         part[chunk][4 * gi + q][l16] = __fadd_rn(__fadd_rn(v[0][gi], v[1][gi]), __fadd_rn(v[2][gi], v[3][gi]));
     __syncthreads();
 
-    const int passes = (G + 15) / 16;
-    for (int idx = threadIdx.x; idx < N * MV_ROWS; idx += blockDim.x) {
-        const int n = idx / MV_ROWS, r = idx - n * MV_ROWS;
-        if (row0 + r >= R) continue;
-        PassTree tr;
-        tree_init(tr);
-        for (int ps = 0; ps < passes; ps++) {
-            float c[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int cc = 4 * ps + k;
-                c[k] = cc < nchunks ? part[cc][n][r] : 0.0f;
-            }
-            tree_push(tr, __fadd_rn(__fadd_rn(c[0], c[1]), __fadd_rn(c[2], c[3])));
-        }
-        mg.y[m][(int64_t)n * mg.ldy[m] + row0 + r] = tree_final(tr);
-    }
+    mv_merge(part, nchunks, G, N, R, row0, mg.y[m], mg.ldy[m]);
 }
 
 template <int TYPE, int LB, bool PRE_ALL, bool SB>

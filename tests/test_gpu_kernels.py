@@ -169,6 +169,7 @@ def test_gemv_q8k_reference_inputs(dev, orc, ty):
     (14, 4088, 4096), (12, 4096, 12288),                    # either side of the 4096-row MFMA threshold
     (12, 1000, 4096),                                       # Q4_K below it: v_dot4 to 3 tokens, then MFMA
     (12, 4096, 8448), (14, 4096, 12032),                    # G = 33 / 47: a last chunk of 1 / 3 super-blocks
+    (14, 4096, 16384), (12, 4104, 14336),                   # G = 64 / 56 on many rows: the plane form's 16 / 14 waves
 ])
 def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
     """Speculative-verify invariant: every row of a batch equals its N = 1 result bit for bit."""

@@ -25,8 +25,9 @@ The producers of the GEMV inputs write the Q8_K activation directly: ``rmsfold_q
 residual add + RMSNorm of Engine.rmsfold, gpu4.py:104-106 / q4_rms, q4.cu:39-46) and
 ``swiglu_q8k`` (q4_silu, q4.cu:36-38, as the FFN launches it, engine.py:287); ``gemv_q8`` then
 runs the named matrices on that Q8_K input with no further quantization.  ``head`` is the output
-head with the greedy pick (Engine.head, engine.py:323-331): the GEMV computes the argmax of the
-logits as it stores them (kq_gemv_q8k_argmax).
+head with the greedy pick (Engine.head, engine.py:323-331): in ``"q8k"`` mode the GEMV computes the
+argmax of the logits as it stores them (kq_gemv_q8k_argmax); in ``"f32"`` mode the fp32 GEMV and
+then the argmax over the logits (kq_gemv, kq_argmax), the reference's gemv([head]) + k_argmax.
 """
 import os
 
@@ -83,11 +84,12 @@ def chunk_from_env():
 class Engine:
     """Every buffer a call uses is allocated here, as the reference engine preallocates its device
     scratch (gpu4.py:70-79): the Q8_K activations of up to max(chunk, 16) rows, the prefill GEMM
-    workspace for any chunk of up to ``chunk`` rows of any of the weights' matrices, the argmax
-    workspace and the logits (as many as the tallest matrix has rows).  No call allocates device
+    workspace (mode "q8k") for any chunk of up to ``chunk`` rows of any of the weights' matrices
+    (or of the listed ``groups``), the argmax workspace and the logits (as many as the tallest
+    matrix has rows).  No call allocates device
     memory, so any call can be captured into a HIP graph, the first one included."""
 
-    def __init__(self, weights, mode="q8k", max_cols=None, chunk=None, batch_max=KQ_MAX_BATCH):
+    def __init__(self, weights, mode="q8k", max_cols=None, chunk=None, batch_max=KQ_MAX_BATCH, groups=None):
         if mode not in ("q8k", "f32"):
             raise ValueError("mode must be 'q8k' or 'f32'")
         if not 1 <= batch_max <= KQ_MAX_BATCH:
@@ -106,19 +108,35 @@ class Engine:
         dev = self.device
         # Q8_K workspace (the reference's reused xp scratch, gpu4.py:70-79)
         self.xq = torch.empty(self.max_rows * (cols // QK) * Q8K_BYTES, dtype=torch.uint8, device=dev)
-        # prefill GEMM workspace: the most any chunk (1..chunk rows) of up to three matrices sharing
-        # an input needs (three of the same shape bound every mix)
-        need = 0
-        if self.chunk:
-            for R, C in shapes:
-                if C <= cols:
-                    need = max(need, max(ops.gemm_f32_multi_workspace_bytes([R, R, R], C, m)
-                                         for m in range(1, self.chunk + 1)))
-        self.gemm_ws = torch.empty(need + 256, dtype=torch.uint8, device=dev) if need else None
+        # prefill GEMM workspace (mode "q8k" only: "f32" prefills row by row): the most any chunk
+        # (1..chunk rows) of the matrix groups gemm will see needs.  With ``groups`` (lists of names
+        # that share an input, e.g. [q, k, v], [gate, up]) it is sized for those, three at a time as
+        # gemm sends them; without, for any three matrices of one shape (which bounds every mix).
+        self.gemm_ws = None
+        if self.chunk and mode == "q8k":
+            if groups is not None:
+                sets = []
+                for g in groups:
+                    Rs = [self.w[n][1] for n in g]
+                    Cs = {self.w[n][2] for n in g}
+                    if len(Cs) != 1:
+                        raise ValueError("matrices of a group must share their column count")
+                    sets += [(Rs[i:i + 3], Cs.pop()) for i in range(0, len(Rs), 3)]
+            else:
+                sets = [([R, R, R], C) for R, C in shapes if C <= cols]
+            need = max([self._gemm_need(Rs, C, self.chunk) for Rs, C in sets] or [0])
+            if need:
+                self.gemm_ws = torch.empty(need + 256, dtype=torch.uint8, device=dev)
         self.argmax_ws = ops.argmax_workspace(dev)
         self.argmax_out = torch.empty(1, dtype=torch.int32, device=dev)
         self.logits = torch.empty(max([R for R, _ in shapes] or [1]), dtype=torch.float32, device=dev)
         self.row = torch.empty(cols, dtype=torch.float32, device=dev)     # embed / dequant output
+
+    @staticmethod
+    def _gemm_need(Rs, C, chunk):
+        """Workspace bytes of the largest of the chunks 1..chunk rows of one group (the K split, and
+        so the partial planes, depend on the chunk's row count)."""
+        return max(ops.gemm_f32_multi_workspace_bytes(Rs, C, m) for m in range(1, chunk + 1))
 
     def _check_out(self, y, R, N=1):
         need = (N - 1) * (y.stride(0) if y.dim() == 2 else R) + R
@@ -195,17 +213,24 @@ class Engine:
     def head(self, name, x, y=None):
         """Greedy next token: y = W_name x (the logits, kept in ``y`` or the engine's preallocated
         buffer) and the index of the largest logit, read back to the host as Engine.head does
-        (engine.py:323-331, gemv + k_argmax); the GEMV finds the argmax itself (kq_gemv_q8k_argmax)."""
+        (engine.py:323-331).  Mode "f32" runs the reference's own sequence: the fp32-activation GEMV,
+        then the argmax over the logits (gemv([head]) + k_argmax, engine.py:326-328; kq_gemv then
+        kq_argmax).  Mode "q8k" quantizes x and the GEMV finds the argmax itself as it stores the
+        logits (kq_gemv_q8k_argmax)."""
         w, R, C, ty = self.w[name]
-        if self.mode != "q8k":
-            raise ValueError("head: the fused greedy pick runs on Q8_K activations (mode 'q8k')")
         if y is None:
             if self.logits.numel() < R:
                 raise ValueError("head: %d logits, the engine holds %d" % (R, self.logits.numel()))
             y = self.logits[:R]
         self._check_out(y, R)
-        xq = self._quantize(x.reshape(1, -1)[:, :C], C)
-        ops.gemv_q8k_argmax(w, R, C, ty, xq, y, self.argmax_ws, self.argmax_out)
+        if x.numel() < C:
+            raise ValueError("head: x holds %d values, the matrix has %d columns" % (x.numel(), C))
+        if self.mode == "f32":
+            ops.gemv(w, R, C, ty, x.reshape(-1), y)
+            ops.argmax(y.reshape(-1)[:R], self.argmax_ws, self.argmax_out)
+        else:
+            xq = self._quantize(x.reshape(1, -1)[:, :C], C)
+            ops.gemv_q8k_argmax(w, R, C, ty, xq, y, self.argmax_ws, self.argmax_out)
         return int(self.argmax_out.cpu()[0])
 
     def feed_rows(self, names, X, outs, batch_max=None):
@@ -221,9 +246,13 @@ class Engine:
             return self.gemv_batch(names, X, outs)
         if not self.chunk:
             mats, outs = self._mats(names, outs)
+            for (_, R, _, _), y in zip(mats, outs):
+                self._check_out(y, R, N)
             for n0 in range(0, N, KQ_MAX_BATCH):
                 n1 = min(N, n0 + KQ_MAX_BATCH)
-                self.gemv_batch(names, X[n0:n1], [y[n0:n1] for y in outs])
+                # a 2-D output is sliced by rows; a flat one holds rows of R
+                views = [y[n0:n1] if y.dim() == 2 else y[n0 * R:n1 * R] for (_, R, _, _), y in zip(mats, outs)]
+                self.gemv_batch(names, X[n0:n1], views)
             return 1
         return self.gemm(names, X, outs)
 
@@ -279,6 +308,13 @@ class Engine:
             return self._rows_f32(mats, X, outs)
         if C > self.max_cols:
             raise ValueError("input of %d columns exceeds the engine workspace (%d)" % (C, self.max_cols))
+        have = 0 if self.gemm_ws is None else self.gemm_ws.numel() - 256
+        for i in range(0, len(mats), 3):
+            need = max(ops.gemm_f32_multi_workspace_bytes([m[1] for m in mats[i:i + 3]], C, mc)
+                       for mc in {min(self.chunk, M), M - (M - 1) // self.chunk * self.chunk})
+            if need > have:
+                raise ValueError("gemm: this call needs %d bytes of GEMM workspace, the engine holds %d (build the "
+                                 "Engine after its weights are added, or list this group in groups=)" % (need, have))
         for m0 in range(0, M, self.chunk):
             mc = min(self.chunk, M - m0)
             # a flat output holds rows of R

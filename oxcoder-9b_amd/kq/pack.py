@@ -16,8 +16,9 @@ messages; ``open_pack`` takes its full-or-size mode from KINDI_Q4_VERIFY unless 
 layout, read with 8 MiB preads through two pinned staging buffers whose copies overlap the next
 read (large tensors by several reader threads over contiguous ranges), a least-recently used byte
 budget that spares the embedding and the head, and POSIX_FADV_DONTNEED after each tensor so the
-host page cache does not keep a second copy.  On a 288 GB MI355X the default budget
-keeps the whole 9B pack (5.6 GB) resident.  ``write_pack`` builds a pack from tensors already in
+host page cache does not keep a second copy.  The budget and the pinning rule come from
+KINDI_Q4_GPU_CACHE_BYTES / KINDI_Q4_PIN_BOUNDARIES as in gpu4.py:21-24 (``cache_config``); on a
+288 GB MI355X the default (unset) budget is unlimited, so the whole 9B pack (5.6 GB) stays resident.  ``write_pack`` builds a pack from tensors already in
 the Kindi layout (the converter from GGUF, q4pack.convert, is not part of this path).
 """
 import concurrent.futures as cf
@@ -42,6 +43,36 @@ PINNED = ("token_embd.weight", "output.weight")
 STAGE_BYTES = 8 << 20
 READERS = 4              # host threads reading one large tensor (each: two pinned buffers, a stream)
 PARALLEL_MIN = 64 << 20  # tensors from this size are read by all READERS
+# Device cache budget from KINDI_Q4_GPU_CACHE_BYTES (gpu4.py:21-22).  The reference accepts
+# 0.9..5.8 GB for an 8 GB card; here the upper bound is the MI355X's 288 GB of HBM, and with the
+# variable unset the budget is unlimited (the reference's default, 5.8 GB, is its card's limit).
+CACHE_MIN, CACHE_MAX = 900_000_000, 288_000_000_000
+PIN_MIN = 1_600_000_000  # the embedding and head are spared only from this budget up (gpu4.py:24)
+
+
+def cache_config(limit=None, pin_boundaries=None, env=None):
+    """(limit, pin_boundaries, disk_bypass) as gpu4.Weights reads them (gpu4.py:21-24).
+
+    * limit: the argument when given; else KINDI_Q4_GPU_CACHE_BYTES when set, which must lie in
+      0.9..288 GB; else unlimited.
+    * pin_boundaries: the argument when given; else KINDI_Q4_PIN_BOUNDARIES (default "1") equal to
+      "1" and a budget of at least 1.6 GB.
+    * disk_bypass: KINDI_Q4_STREAM == "1".  On the device path it changes nothing (the budget alone
+      forces eviction), as in the reference's CUDA engine.
+    """
+    env = os.environ if env is None else env
+    if limit is None:
+        v = env.get("KINDI_Q4_GPU_CACHE_BYTES")
+        if v is None:
+            limit = 1 << 62
+        else:
+            limit = int(v)
+            if not CACHE_MIN <= limit <= CACHE_MAX:
+                raise ValueError("GPU tensor cache must be 0.9..288 GB")
+    limit = int(limit)
+    if pin_boundaries is None:
+        pin_boundaries = env.get("KINDI_Q4_PIN_BOUNDARIES", "1") == "1" and limit >= PIN_MIN
+    return limit, bool(pin_boundaries), env.get("KINDI_Q4_STREAM", "0") == "1"
 
 
 def profile_shapes(layers=32):
@@ -175,15 +206,14 @@ def write_pack(out, tensors, dims=PROFILE_DIMS, model="synthetic"):
 class PackWeights:
     """Device tensor cache over a pack: ``w[name] -> (buf, R, C, type)`` (gpu4.py:25-48)."""
 
-    def __init__(self, pack, index=None, limit=None, device="cuda", pin_boundaries=True):
+    def __init__(self, pack, index=None, limit=None, device="cuda", pin_boundaries=None):
         self.pack = Path(pack)
         self.device = torch.device(device)
         self.index = index if index is not None else json.loads((self.pack / "index.json").read_text())["tensors"]
         self.fd = os.open(str(self.pack / "weights.bin"), os.O_RDONLY)
         self.cache = OrderedDict()
         self.used = self.read_bytes = self.hits = self.misses = 0
-        self.limit = int(limit) if limit is not None else 1 << 62
-        self.pin_boundaries = pin_boundaries
+        self.limit, self.pin_boundaries, self.disk_bypass = cache_config(limit, pin_boundaries)
         self._stage = None
         self._pool = None
         self._f32 = {}
@@ -294,8 +324,9 @@ class PackWeights:
         return self._f32[name]
 
 
-def open_pack(pack, full=None, limit=None, device="cuda", dims=PROFILE_DIMS, shapes=None):
+def open_pack(pack, full=None, limit=None, device="cuda", dims=PROFILE_DIMS, shapes=None, pin_boundaries=None):
     """verify_pack, then a PackWeights over the pack (the Engine's weights, gpu4.py:55-59).
-    ``full=None`` takes the mode from KINDI_Q4_VERIFY, as the Engine does."""
+    ``full=None`` takes the mode from KINDI_Q4_VERIFY, as the Engine does; ``limit`` and
+    ``pin_boundaries`` left None come from the environment (cache_config)."""
     verify_pack(pack, full=verification_full() if full is None else full, dims=dims, shapes=shapes)
-    return PackWeights(pack, limit=limit, device=device)
+    return PackWeights(pack, limit=limit, device=device, pin_boundaries=pin_boundaries)

@@ -123,6 +123,32 @@ def test_head_151936_q6k(dev, orc, head_q6k, seed):
         assert top == int(np.argmax(ref))
 
 
+@pytest.mark.parametrize("seed", [0, 3])
+def test_engine_head_f32_151936_q6k(dev, orc, head_q6k, seed):
+    """Engine.head in the reference's numerics (mode "f32"): the fp32-activation GEMV, then the
+    argmax over its logits, as Engine.head runs gemv([head]) + k_argmax (engine.py:326-328).  The
+    logits within the bar of the oracle's restatement of q4_dot (kc_matvec bit for bit), the pick
+    the oracle's k_argmax of the logits."""
+    from kq.gpu4 import Engine, Weights
+    W, wd, R, C = head_q6k
+    print("engine head f32 seed", seed, flush=True)
+    w = Weights(dev)
+    w.cache["output.weight"] = (wd, R, C, 14)
+    eng = Engine(w, mode="f32", chunk=0)
+    x = kqq.synthetic_activations(1, C, seed=seed)[0]
+    top = eng.head("output.weight", dev_t(x, dev))
+    logits = host(eng.logits[:R])
+    ref = orc.matvec_f32(W, R, C, 14, x)
+    assert_close_inf(logits, ref.astype(np.float64), "head f32")
+    assert top == orc.argmax(logits)
+    srt = np.sort(ref)
+    if srt[-1] - srt[-2] > 2 * TOL * np.abs(ref).max():
+        assert top == int(np.argmax(ref))
+    y = torch.empty(R, device=dev)                          # a caller's logits buffer
+    assert eng.head("output.weight", dev_t(x, dev), y) == top
+    np.testing.assert_array_equal(host(y), logits)
+
+
 def random_q4k_blocks(R, C, seed):
     """Random Q4_K block bytes (any scale/min pattern) with d, dmin drawn from fp16 values of the
     size a N(0, 0.02) row gives, in the Kindi layout."""

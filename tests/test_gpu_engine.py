@@ -280,12 +280,17 @@ def test_engine_feed_rows_without_chunked_prefill(layer, dev, monkeypatch):
     X = torch.from_numpy(kqq.synthetic_activations(37, 4096, seed=4)).to(dev)
     y = torch.empty((37, 1024), device=dev)
     eng.feed_rows(["attn_k"], X, [y])
+    flat = torch.empty(37 * 1024, device=dev)                # a flat output holds rows of R
+    eng.feed_rows(["attn_k"], X, [flat])
     for n in (0, 16, 36):
         one = torch.empty(1024, device=dev)
         eng.gemv(["attn_k"], X[n], [one])
         assert torch.equal(y[n], one), n
+        assert torch.equal(flat[n * 1024:(n + 1) * 1024], one), n
     with pytest.raises(ValueError, match="chunked prefill is off"):
         eng.gemm(["attn_k"], X, [y])
+    with pytest.raises(ValueError, match="output buffer too small"):
+        eng.feed_rows(["attn_k"], X, [torch.empty(36 * 1024, device=dev)])
 
 
 @pytest.mark.parametrize("mode", ["q8k", "f32"])

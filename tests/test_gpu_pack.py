@@ -34,7 +34,8 @@ def shapes():
 
 def test_pack_weights_bytes_and_budget(dev, built):
     p, tensors = built
-    w = pack.open_pack(p, full=True, limit=60_000_000, device=dev, dims=DIMS, shapes=shapes())
+    # an explicit budget below 1.6 GB would not pin by the reference's rule (gpu4.py:24): pin here
+    w = pack.open_pack(p, full=True, limit=60_000_000, device=dev, dims=DIMS, shapes=shapes(), pin_boundaries=True)
     for name in ("token_embd.weight", "output.weight", "blk.0.ffn_gate.weight"):
         buf, R, C, ty = w[name]
         assert (R, C, ty) == tensors[name][1:] and buf.is_cuda

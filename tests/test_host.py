@@ -273,3 +273,14 @@ def test_bench_refuses_what_it_does_not_measure(args, code, text):
     assert r.returncode == code, (r.returncode, r.stderr)
     assert text in r.stderr
     assert r.stdout == ""
+
+
+def test_argmax_workspace_size_in_the_docs():
+    """The argmax workspace size that the header and the integration guide state is what the
+    library asks for: a caller who sizes the buffer from the documents gets enough bytes."""
+    from kq import _lib
+    n = int(_lib.kq().kq_argmax_workspace())
+    for doc in ("include/kq.h", "INTEGRATION.md"):
+        text = open(os.path.join(ROOT, doc)).read()
+        stated = {int(v) for v in re.findall(r"kq_argmax_workspace\(\)`? bytes \((\d+)", text)}
+        assert stated == {n}, (doc, stated, n)

@@ -254,3 +254,90 @@ def test_side_readers_wait_for_the_callers_stream(tiny_pack, monkeypatch):
         assert all(i < first_read for i, e in enumerate(events) if e[0] == "wait")
     finally:
         w.close()
+
+
+@pytest.mark.parametrize("env,limit,pin", [
+    ({}, 1 << 62, True),                                                   # unset: unlimited, pinned
+    ({"KINDI_Q4_GPU_CACHE_BYTES": "5800000000"}, 5_800_000_000, True),     # the reference's default
+    ({"KINDI_Q4_GPU_CACHE_BYTES": "1600000000"}, 1_600_000_000, True),     # pinning starts at 1.6 GB
+    ({"KINDI_Q4_GPU_CACHE_BYTES": "1599999999"}, 1_599_999_999, False),
+    ({"KINDI_Q4_GPU_CACHE_BYTES": "900000000"}, 900_000_000, False),       # the lower bound
+    ({"KINDI_Q4_GPU_CACHE_BYTES": "288000000000"}, 288_000_000_000, True),  # the MI355X's HBM
+    ({"KINDI_Q4_GPU_CACHE_BYTES": "5800000000", "KINDI_Q4_PIN_BOUNDARIES": "0"}, 5_800_000_000, False),
+    ({"KINDI_Q4_PIN_BOUNDARIES": "yes"}, 1 << 62, False),                  # only "1" pins, as gpu4.py:24
+])
+def test_cache_config_follows_the_reference_variables(env, limit, pin):
+    """KINDI_Q4_GPU_CACHE_BYTES and KINDI_Q4_PIN_BOUNDARIES read as gpu4.Weights reads them
+    (gpu4.py:21-24), with the budget's upper bound widened to 288 GB and no budget when unset."""
+    assert pack.cache_config(env=env)[:2] == (limit, pin)
+    assert pack.cache_config(env=dict(env, KINDI_Q4_STREAM="1"))[2] is True
+    assert pack.cache_config(env=env)[2] is False
+
+
+@pytest.mark.parametrize("value", ["899999999", "288000000001", "0", "-5"])
+def test_cache_budget_out_of_range_is_an_error(value):
+    with pytest.raises(ValueError, match="GPU tensor cache must be 0.9..288 GB"):
+        pack.cache_config(env={"KINDI_Q4_GPU_CACHE_BYTES": value})
+
+
+def test_cache_arguments_override_the_environment():
+    """Explicit arguments win over the variables (tests use budgets below the range); an explicit
+    budget still follows the pinning rule unless pinning is given too."""
+    env = {"KINDI_Q4_GPU_CACHE_BYTES": "5", "KINDI_Q4_PIN_BOUNDARIES": "1"}
+    assert pack.cache_config(limit=60_000_000, env=env)[:2] == (60_000_000, False)
+    assert pack.cache_config(limit=60_000_000, pin_boundaries=True, env=env)[:2] == (60_000_000, True)
+    assert pack.cache_config(limit=2_000_000_000, env={})[:2] == (2_000_000_000, True)
+
+
+@pytest.mark.parametrize("pin,evicted", [(True, "blk.0.ffn_gate.weight"), (False, "token_embd.weight")])
+def test_eviction_spares_the_boundaries_only_when_pinned(tiny_pack, monkeypatch, pin, evicted):
+    """The LRU budget evicts the oldest tensor that is not the embedding or the head when pinning
+    is on (gpu4.py:33-35), the oldest of all when it is off.  Host only: the cache holds stand-ins."""
+    monkeypatch.setenv("KINDI_Q4_GPU_CACHE_BYTES", "1000000000")
+    monkeypatch.setenv("KINDI_Q4_PIN_BOUNDARIES", "1" if pin else "0")
+    import torch
+    w = pack.PackWeights(tiny_pack, device="cpu")
+    try:
+        assert w.limit == 1_000_000_000 and w.pin_boundaries is False     # below 1.6 GB: never pinned
+        w.pin_boundaries = pin
+        w.limit = 300
+        for name in ("token_embd.weight", "blk.0.ffn_gate.weight", "output.weight"):
+            w.cache[name] = (torch.empty(100, dtype=torch.uint8), 0, 0, 12)
+            w.used += 100
+        w._evict_for(100)
+        assert evicted not in w.cache and len(w.cache) == 2 and w.used == 200
+    finally:
+        w.close()
+
+
+def test_engine_gemm_workspace_by_mode_and_groups(tiny_pack):
+    """Mode "f32" keeps no GEMM workspace (it prefills row by row); with ``groups`` the workspace
+    is sized for the groups gemm will see, three matrices at a time.  Host only."""
+    from kq import ops
+    from kq.gpu4 import Engine
+    w = pack.PackWeights(tiny_pack, device="cpu")
+    try:
+        assert Engine(w, mode="f32").gemm_ws is None
+        for name in ("token_embd.weight", "output.weight", "blk.0.ffn_down.weight"):
+            w.cache[name] = (None,) + tuple(int(w.index[name][k]) for k in ("rows", "ne0", "type"))
+        g = [["token_embd.weight", "output.weight"], ["blk.0.ffn_down.weight"]]
+        eng = Engine(w, mode="q8k", groups=g)
+        need = max(max(ops.gemm_f32_multi_workspace_bytes(Rs, C, m) for m in range(1, 257))
+                   for Rs, C in [([16, 16], 256), ([8], 512)])
+        assert eng.gemm_ws.numel() == need + 256
+        with pytest.raises(ValueError, match="share their column count"):
+            Engine(w, mode="q8k", groups=[["output.weight", "blk.0.ffn_down.weight"]])
+    finally:
+        w.close()
+
+
+def test_engine_built_before_its_weights_rejects_gemm():
+    """An Engine over weights that are added after it was built has no GEMM workspace for them:
+    gemm says so instead of failing on a null workspace.  Host only (rejected before any launch)."""
+    import torch
+    from kq.gpu4 import Engine, Weights
+    w = Weights("cpu")
+    eng = Engine(w, mode="q8k")
+    w.add("m", np.zeros(16 * 144, np.uint8), 16, 256, 12)
+    with pytest.raises(ValueError, match="GEMM workspace"):
+        eng.gemm(["m"], torch.zeros(20, 256), [torch.empty(20, 16)])

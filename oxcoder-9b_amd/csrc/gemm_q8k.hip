@@ -488,6 +488,519 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
         }
 }
 
+// ------------------------------------------------------------------ pipelined kernel
+// A workgroup of 8 waves (512 threads, one workgroup per CU) owns 256 tokens x 64 weight rows;
+// wave w takes tokens 32w..32w+31 against all 64 rows (two 32x32 MFMA tiles sharing the A
+// operand).  The 8 waves share one unpack of the weight planes per super-block (each thread
+// unpacks an eighth of a row: 32 codes), so each unpacked plane byte serves 256 tokens.
+//
+// Epilogue pipelining.  The fp32 epilogue of super-block g-1 (convert, scale, min term,
+// accumulate: 4 VALU instructions per output and lane) runs while the MFMAs of super-block g are
+// in flight, from the previous super-block's integer accumulators (acc_prev) and its scales in
+// LDS.  Each wave therefore issues an even mix of MFMA and VALU work instead of alternating
+// MFMA-only sweeps with VALU-only epilogues.  Weight planes are double-buffered (the next
+// super-block is unpacked during this one); the scale arrays are triple-buffered, since the
+// epilogue of g-1 still reads them while the unpack of g+1 writes.  One barrier per super-block.
+constexpr int GP_BM = 256, GP_BN = 64, GP_THREADS = 512;
+#ifndef KQ_GP_AHEAD
+#define KQ_GP_AHEAD 2       // B operands are read this many int8 MFMAs ahead of their use
+#endif
+#ifndef KQ_GP_PRIO
+#define KQ_GP_PRIO 0        // wave priority while issuing each MFMA (0: unchanged)
+#endif
+
+// Plane rows are padded to 272 B (68 dwords): consecutive rows start 4 banks apart, so the 16-byte
+// reads of 16 consecutive rows fall on distinct banks, and every address is the row's base plus an
+// immediate offset (no per-chunk address registers, as an XOR swizzle would need).
+constexpr int GP_ROW = 272;
+__device__ __forceinline__ int prw(int r, int c) { return r * GP_ROW + c * 16; }
+struct PlaneBuf {                   // one super-block's weight planes: 64 rows of 256 B each
+    int8_t wh[GP_BN * GP_ROW];
+    int8_t wl[GP_BN * GP_ROW];
+};
+// Min-term operand rows are padded to 12 dwords: the 16-byte reads of 16 consecutive rows then
+// cover distinct banks (a stride of 8 dwords made every other read collide).
+constexpr int GP_MROW = 12;
+struct ScaleBuf {                   // one super-block's scales
+    uint32_t wmin[GP_BN * GP_MROW]; // Q4_K: row n = 16 f16 [-64 m_0..7, -m_0..7] (+ padding)
+    uint32_t xmin[GP_BM * GP_MROW]; // Q4_K: token m = 16 f16 [B_0..7 >> 6, B_0..7 & 63] (+ padding)
+    float d[GP_BN], dm[GP_BN], dx[GP_BM];
+};
+
+// Raw bytes of one eighth of a weight row (part pi = 0..7) for one super-block.
+//   Q4_K: qs bytes 32p + 16cc .. +15 (p = pi >> 1, cc = pi & 1): elements 64p + 16cc + 0..15 (low
+//         nibbles, sub-block 2p) and 64p + 32 + 16cc + 0..15 (high nibbles, sub-block 2p+1).
+//   Q6_K: half h = pi >> 2, slice jj = (pi >> 1) & 1, c = pi & 1: elements 128h + 32k + 16jj + 0..15
+//         for k = c and c + 2 (ql bytes 64h + 32c + 16jj, low / high nibble; qh bytes 32h + 16jj,
+//         bits 2k; scales 8h + 2k + jj).
+template <int TYPE> struct RawP;
+template <> struct RawP<TYPE_Q4_K> { u32x4 hdr, q; };
+template <> struct RawP<TYPE_Q6_K> {
+    Chunk20 ql, qh;
+    u32x2 sc;
+    uint32_t sce, dw, sh;
+};
+
+// Raw buffer loads: a descriptor over the whole buffer in scalar registers, a per-lane byte offset
+// that stays the same for every super-block, a scalar per-super-block offset, and the field offset as
+// an immediate, so the loop does no 64-bit address arithmetic.  Word 3 of the descriptor is the one
+// every gfx950 raw buffer here uses (32-bit data format); loads past num_records return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bld16(__amdgpu_buffer_rsrc_t r, int v, int s) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0));
+}
+__device__ __forceinline__ u32x2 bld8(__amdgpu_buffer_rsrc_t r, int v, int s) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, v, s, 0));
+}
+__device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, int v, int s) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0);
+}
+
+// Lane offsets of one part's fields within its weight block (add the super-block's g * 8 * BS as
+// the scalar offset).  Q6_K: a block of row r starts at 2 (r & 1) (mod 4) in the tile column, so
+// every field is read from the dword at or below it and funnel-shifted by sh = 2 (r & 1); the bytes
+// read past a block (at most 2, only when sh = 0) belong to the next row of the tile column.
+template <int TYPE> struct PartOff;
+template <> struct PartOff<TYPE_Q4_K> {
+    int hdr, q;
+    __device__ __forceinline__ PartOff(int blk, int pi, int) : hdr(blk), q(blk + 16 + 16 * pi) {}
+};
+template <> struct PartOff<TYPE_Q6_K> {
+    int ql, qh, sc, base;
+    uint32_t sh;
+    __device__ __forceinline__ PartOff(int blk, int pi, int row) {
+        const int h = pi >> 2, jj = (pi >> 1) & 1, c = pi & 1;
+        sh = 2u * (uint32_t)(row & 1);
+        base = blk - (int)sh;
+        ql = base + 64 * h + 32 * c + 16 * jj;
+        qh = base + 128 + 32 * h + 16 * jj;
+        sc = base + 192 + 8 * h;
+    }
+};
+
+__device__ __forceinline__ void load_rawp(RawP<TYPE_Q4_K>& r, __amdgpu_buffer_rsrc_t wr, const PartOff<TYPE_Q4_K>& o,
+                                          int soff) {
+    r.hdr = bld16(wr, o.hdr, soff);
+    r.q = bld16(wr, o.q, soff);
+}
+__device__ __forceinline__ void load_rawp(RawP<TYPE_Q6_K>& r, __amdgpu_buffer_rsrc_t wr, const PartOff<TYPE_Q6_K>& o,
+                                          int soff) {
+    r.sh = o.sh;
+    r.ql = Chunk20{bld16(wr, o.ql, soff), bld4(wr, o.ql + 16, soff)};
+    r.qh = Chunk20{bld16(wr, o.qh, soff), bld4(wr, o.qh + 16, soff)};
+    r.sc = bld8(wr, o.sc, soff);
+    r.sce = bld4(wr, o.sc + 8, soff);
+    r.dw = bld4(wr, o.base + 208, soff);
+}
+
+// Activation side of the pipelined kernel: two threads per token row, part xp holding bsums
+// 8xp .. 8xp+7 and the row's d.
+__device__ __forceinline__ void load_xp(RawX<2>& r, __amdgpu_buffer_rsrc_t xr, int vrow, int xp, int soff) {
+    const u32x4 v = bld16(xr, vrow + 260 + 16 * xp, soff);
+    r.bs[0] = v.x; r.bs[1] = v.y; r.bs[2] = v.z; r.bs[3] = v.w;
+    r.d = bld4(xr, vrow, soff);
+}
+
+// The unpack of one part, in chunks that the step spreads over its MFMA slots.
+template <int TYPE> struct UnpackP;
+template <> struct UnpackP<TYPE_Q4_K> {
+    static constexpr int NCHUNK = 3;
+    uint32_t alo, blo, ahi, bhi;
+    // chunk 0: scales and mins of sub-blocks 2p, 2p+1, the min operands, d and dmin; chunk 1: the
+    // low nibbles (sub-block 2p) into both planes; chunk 2: the high nibbles (sub-block 2p+1)
+    template <int C>
+    __device__ __forceinline__ void chunk(const RawP<TYPE_Q4_K>& r, int pi, int row, PlaneBuf& Lp, ScaleBuf& Ls) {
+        const int p = pi >> 1, cc = pi & 1;
+        if constexpr (C == 0) {
+            const ScMin sm = q4k_scmin_pair(r.hdr.y, r.hdr.z, r.hdr.w, p);
+            alo = (sm.sc_lo >> 3) * 0x10001u;
+            blo = (sm.sc_lo & 7u) * 0x10001u;
+            ahi = (sm.sc_hi >> 3) * 0x10001u;
+            bhi = (sm.sc_hi & 7u) * 0x10001u;
+            // both halves (cc) of a sub-block pair store the same min operands, every part the same d
+            const float mlo = (float)sm.m_lo, mhi = (float)sm.m_hi;
+            Ls.wmin[row * GP_MROW + p] = pk_f16(-64.0f * mlo, -64.0f * mhi);
+            Ls.wmin[row * GP_MROW + 4 + p] = pk_f16(-mlo, -mhi);
+            Ls.d[row] = f16_lo(r.hdr.x);
+            Ls.dm[row] = f16_hi(r.hdr.x);
+        } else {
+            const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+            const uint32_t a = C == 1 ? alo : ahi, b = C == 1 ? blo : bhi;
+            uint32_t hp[4], lp[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t q = (C == 1 ? w[i] : w[i] >> 4) & 0x0f0f0f0fu;
+                hp[i] = mul_u8x4(q, a);
+                lp[i] = mul_u8x4(q, b);
+            }
+            const int ch = 4 * p + 2 * (C - 1) + cc;           // elements 64p + 32(C-1) + 16cc + 0..15
+            st16(Lp.wh + prw(row, ch), hp[0], hp[1], hp[2], hp[3]);
+            st16(Lp.wl + prw(row, ch), lp[0], lp[1], lp[2], lp[3]);
+        }
+    }
+};
+template <> struct UnpackP<TYPE_Q6_K> {
+    static constexpr int NCHUNK = 9;
+    uint32_t Lw[4], Hw[4];
+    uint32_t s2[2], c2[2];
+    uint32_t hb[4], lb[4];
+    // chunk 0: the funnel shifts, the two slices' scales, d; chunk 1 + 4kk + i: dword i of slice
+    // k = c + 2kk; chunks 4 and 8 store the slice's two 16-byte plane pieces
+    template <int C>
+    __device__ __forceinline__ void chunk(const RawP<TYPE_Q6_K>& r, int pi, int row, PlaneBuf& Lp, ScaleBuf& Ls) {
+        const int h = pi >> 2, jj = (pi >> 1) & 1, c = pi & 1;
+        const uint32_t sh = r.sh;
+        if constexpr (C == 0) {
+            const uint32_t s0 = __builtin_amdgcn_alignbyte(r.sc.y, r.sc.x, sh);   // scales 8h .. 8h+3
+            const uint32_t s1 = __builtin_amdgcn_alignbyte(r.sce, r.sc.y, sh);    // scales 8h+4 .. 8h+7
+            Lw[0] = __builtin_amdgcn_alignbyte(r.ql.v.y, r.ql.v.x, sh);
+            Lw[1] = __builtin_amdgcn_alignbyte(r.ql.v.z, r.ql.v.y, sh);
+            Lw[2] = __builtin_amdgcn_alignbyte(r.ql.v.w, r.ql.v.z, sh);
+            Lw[3] = __builtin_amdgcn_alignbyte(r.ql.e, r.ql.v.w, sh);
+            Hw[0] = __builtin_amdgcn_alignbyte(r.qh.v.y, r.qh.v.x, sh);
+            Hw[1] = __builtin_amdgcn_alignbyte(r.qh.v.z, r.qh.v.y, sh);
+            Hw[2] = __builtin_amdgcn_alignbyte(r.qh.v.w, r.qh.v.z, sh);
+            Hw[3] = __builtin_amdgcn_alignbyte(r.qh.e, r.qh.v.w, sh);
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {      // scale 8h + 2k + jj, k = c + 2kk: byte 2c + jj of s0 / s1
+                const int sc = (int)(int8_t)(uint8_t)((kk ? s1 : s0) >> (8 * (2 * c + jj)));
+                s2[kk] = (uint32_t)(sc & 0xffff) * 0x10001u;
+                c2[kk] = (uint32_t)((128 - 32 * sc) & 0xffff) * 0x10001u;
+            }
+            Ls.d[row] = f16_lo(r.dw >> (8 * sh));         // same value from every part of the row
+        } else {
+            constexpr int kk = (C - 1) >> 2, i = (C - 1) & 3;
+            const int k = c + 2 * kk;
+            const uint32_t lq = (Lw[i] >> (4 * kk)) & 0x0f0f0f0fu;
+            const uint32_t hq = ((Hw[i] >> (2 * k)) & 0x03030303u) << 4;
+            const uint32_t q = lq | hq;                                          // 6-bit codes, 4 bytes
+            const uint32_t e = __builtin_amdgcn_perm(0u, q, 0x0c020c00u);        // bytes 0, 2 -> 16-bit lanes
+            const uint32_t o = __builtin_amdgcn_perm(0u, q, 0x0c030c01u);        // bytes 1, 3
+            const s16x2 sv = __builtin_bit_cast(s16x2, s2[kk]), cv = __builtin_bit_cast(s16x2, c2[kk]);
+            const uint32_t ve = __builtin_bit_cast(uint32_t, (s16x2)(__builtin_bit_cast(s16x2, e) * sv + cv));
+            const uint32_t vo = __builtin_bit_cast(uint32_t, (s16x2)(__builtin_bit_cast(s16x2, o) * sv + cv));
+            hb[i] = __builtin_amdgcn_perm(vo, ve, 0x07030501u);                  // high bytes, element order
+            lb[i] = __builtin_amdgcn_perm(vo, ve, 0x06020400u) ^ 0x80808080u;
+            if constexpr (i == 3) {
+                const int ch = 8 * h + 2 * k + jj;
+                st16(Lp.wh + prw(row, ch), hb[0], hb[1], hb[2], hb[3]);
+                st16(Lp.wl + prw(row, ch), lb[0], lb[1], lb[2], lb[3]);
+            }
+        }
+    }
+};
+
+// Activation side: two threads per token row (xp = 0, 1), each holding four of the eight Q4_K
+// sub-block sums B_s (bsums 8xp .. 8xp+7) and the row's d.
+__device__ __forceinline__ void stage_xp(const RawX<2>& r, int mr, int xp, bool q4, ScaleBuf& Ls) {
+    if (q4) {
+        int B[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) B[i] = (int)(int16_t)(r.bs[i] & 0xffffu) + (int)(int16_t)(r.bs[i] >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; i += 2) {
+            const int dw = mr * GP_MROW + (4 * xp + i) / 2;
+            Ls.xmin[dw] = pk_f16((float)(B[i] >> 6), (float)(B[i + 1] >> 6));
+            Ls.xmin[dw + 4] = pk_f16((float)(B[i] & 63), (float)(B[i + 1] & 63));
+        }
+    }
+    Ls.dx[mr] = __builtin_bit_cast(float, r.d);
+}
+
+// The step's slot program: one MFMA per slot, in this order, and the slot of every other piece of
+// work.  MFMA codes: 0..15 the high-plane sweep (tile t, K step ks: 8t + ks), 16..31 the low-plane
+// sweep (16 + 8t + ks), 32 / 33 the min-term MFMA of the tile 0 / tile 1 epilogue (Q4_K).
+//
+// Epilogues are staggered by tile: tile 0's sums are complete once its low-plane sweep ends, so
+// its epilogue (E[0], from this super-block's scales) runs under tile 1's low-plane MFMAs of the
+// same step; tile 1's epilogue (E[1]) runs in the next step, from the previous super-block's sums
+// and scales.  Only one tile's sums are pending across a barrier.
+//
+// Constraints the slots keep: a tile's shift after its last high-plane MFMA (two slots of latency)
+// and before its first low-plane MFMA; a min-term MFMA after its operand reads (ER) and before the
+// epilogue that uses it; tile 0's epilogue after its last low-plane MFMA; the raw loads of
+// super-block g+2 after the unpack has consumed g+1's; each A operand reloaded after its last use.
+template <int TYPE> struct GpSched;
+template <> struct GpSched<TYPE_Q4_K> {
+    static constexpr int NSLOT = 34;
+    static constexpr int mf[NSLOT] = {0, 1, 2, 3, 33, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 16, 17,
+                                      18, 19, 14, 15, 32, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31};
+    static constexpr int U[3] = {0, 1, 2};
+    static constexpr int RAW = 3, XS = 3;
+    static constexpr int ER[2] = {17, 0};
+    static constexpr int E[2][8] = {{27, 28, 29, 30, 31, 32, 33, 33}, {6, 7, 8, 9, 10, 11, 12, 13}};
+    static constexpr int SH[2][2] = {{11, 12}, {22, 23}};
+    static constexpr int A[8] = {26, 27, 28, 29, 30, 31, 32, 33};
+};
+template <> struct GpSched<TYPE_Q6_K> {
+    static constexpr int NSLOT = 32;
+    static constexpr int mf[NSLOT] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 16, 17,
+                                      18, 19, 14, 15, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31};
+    static constexpr int U[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
+    static constexpr int RAW = 8, XS = 8;
+    static constexpr int ER[2] = {20, 9};
+    static constexpr int E[2][8] = {{25, 26, 27, 28, 29, 30, 31, 31}, {11, 12, 13, 14, 15, 16, 17, 18}};
+    static constexpr int SH[2][2] = {{10, 11}, {21, 22}};
+    static constexpr int A[8] = {24, 25, 26, 27, 28, 29, 30, 31};
+};
+// position of slot s among the int8 MFMAs (codes < 32), and the slot of position p
+template <class SC> __host__ __device__ constexpr int gp_pos(int s) {
+    int p = 0;
+    for (int j = 0; j < s; j++) p += SC::mf[j] < 32;
+    return p;
+}
+template <class SC> __host__ __device__ constexpr int gp_code_at(int p) {
+    for (int j = 0; j < SC::NSLOT; j++)
+        if (SC::mf[j] < 32 && gp_pos<SC>(j) == p) return SC::mf[j];
+    return -1;
+}
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+template <int TYPE, bool FRAG>
+__global__ void __launch_bounds__(GP_THREADS)
+k_gemm_q8k_p(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* __restrict__ XF, int M) {
+    constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    constexpr int SHIFT = TYPE == TYPE_Q4_K ? 3 : 8;
+    __shared__ __attribute__((aligned(16))) PlaneBuf LP0;
+    __shared__ __attribute__((aligned(16))) PlaneBuf LP1;
+    __shared__ __attribute__((aligned(16))) ScaleBuf LS0;
+    __shared__ __attribute__((aligned(16))) ScaleBuf LS1;
+    __shared__ __attribute__((aligned(16))) ScaleBuf LS2;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = lane >> 5, l32 = lane & 31;
+    const int bx = blockIdx.x;
+    const int mi = gg.n > 1 && bx >= gg.m[1].wg0 ? (gg.n > 2 && bx >= gg.m[2].wg0 ? 2 : 1) : 0;
+    auto field = [&](auto get) { return mi == 0 ? get(gg.m[0]) : mi == 1 ? get(gg.m[1]) : get(gg.m[2]); };
+    const uint8_t* const W = field([](const GemmMat& g) { return g.w; });
+    float* const Y = field([](const GemmMat& g) { return g.y; });
+    float* const P = field([](const GemmMat& g) { return g.part; });
+    const int64_t ldy = field([](const GemmMat& g) { return g.ldy; });
+    const int R = field([](const GemmMat& g) { return g.R; });
+    const int ntile = field([](const GemmMat& g) { return g.ntile; });
+    const int gps = field([](const GemmMat& g) { return g.gps; });
+    const int local = bx - field([](const GemmMat& g) { return g.wg0; });
+    const int split = local / ntile;
+    const int n0 = (local - split * ntile) * GP_BN, m0 = blockIdx.y * GP_BM;
+    const int64_t xrow = (int64_t)G * Q8K_BYTES;
+    const int gbeg = split * gps, gend = gbeg + gps < G ? gbeg + gps : G;
+    float* const Yo = P ? P + (int64_t)split * M * R : Y;
+    const int64_t ldo = P ? (int64_t)R : ldy;
+
+    // A operand of this lane for K step ks of super-block g: byte aoff + (ks & 4) * AK of the A buffer,
+    // plus g * AG (scalar) and (ks & 3) * AK (immediate)
+    constexpr int AG = FRAG ? 8192 : Q8K_BYTES, AK = FRAG ? 1024 : 32;
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(XQ, (uint32_t)M * (uint32_t)xrow);
+    const __amdgpu_buffer_rsrc_t ar = FRAG ? buf_rsrc(XF, (uint32_t)((M + GP_BM - 1) / GP_BM * GP_BM) * (uint32_t)G * QK) : xr;
+    int aoff;
+    if (FRAG) {
+        aoff = ((blockIdx.y * (GP_BM / 32) + wave) * G * 512 + lane) * 16;
+    } else {
+        int m = m0 + 32 * wave + l32;
+        m = m < M ? m : M - 1;
+        aoff = m * (int)xrow + 4 + 16 * half;
+    }
+    const int aoff4 = aoff + 4 * AK;
+    auto load_a = [&](int ks, int g) {
+        return __builtin_bit_cast(v4i, bld16(ar, (ks < 4 ? aoff : aoff4) + (ks & 3) * AK, g * AG));
+    };
+    // activation row staged by this thread (two threads per row)
+    const int mr = tid & (GP_BM - 1), xp = tid >> 8;
+    const int xoff = (m0 + mr < M ? m0 + mr : M - 1) * (int)xrow;
+    // weight row part unpacked by this thread: wave w unpacks rows 8w..8w+7 (one tile column),
+    // eight lanes per row.  The two rows of a 16-lane group are 4 (Q6_K) or 2 (Q4_K) rows apart, so
+    // their plane stores (chunk sets offset by that many 16-byte chunks) fall on distinct banks.
+    const int pj = lane >> 3;
+    const int prow = 8 * wave + (TYPE == TYPE_Q6_K ? ((pj & 1) << 2 | pj >> 1) : ((pj & 1) << 1 | (pj & 4) | (pj >> 1 & 1))),
+              pi = lane & 7;
+    const int pr = n0 + prow < R ? n0 + prow : R - 1;
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(W, (uint32_t)R * (uint32_t)G * BS);
+    const PartOff<TYPE> po(((pr >> 3) * G * 8 + (pr & 7)) * BS, pi, pr);
+
+    float yacc[2][16];
+    // integer sums: tile 0's are consumed within their step; tile 1's are pending into the next
+    // step, so they have one set per step parity (a step writes its own while the epilogue reads
+    // the other; no copy between steps)
+    v16i acc0, acc1s[2];
+    acc1s[1] = v16i{};
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int a = 0; a < 16; a++) yacc[t][a] = 0.0f;
+    // the first step's pending epilogue reads LS2: zero scales make it add nothing
+    for (int i = tid; i < (int)(sizeof(ScaleBuf) / 4); i += GP_THREADS) reinterpret_cast<uint32_t*>(&LS2)[i] = 0u;
+
+    RawP<TYPE> raw;
+    RawX<2> rx;
+    UnpackP<TYPE> up;
+    v4i afr[8];
+    load_rawp(raw, wr, po, gbeg * 8 * BS);
+    load_xp(rx, xr, xoff, xp, gbeg * Q8K_BYTES);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) afr[ks] = load_a(ks, gbeg);
+    static_for<0, UnpackP<TYPE>::NCHUNK>([&](auto c) { up.template chunk<decltype(c)::value>(raw, pi, prow, LP0, LS0); });
+    stage_xp(rx, mr, xp, TYPE == TYPE_Q4_K, LS0);
+    {
+        const int g1 = gbeg + 1 < gend ? gbeg + 1 : gbeg;
+        load_rawp(raw, wr, po, g1 * 8 * BS);
+        load_xp(rx, xr, xoff, xp, g1 * Q8K_BYTES);
+    }
+    __syncthreads();
+
+    const int nrow[2] = {l32, 32 + l32};     // this lane's B rows (weight rows within the tile)
+
+    // per pending tile: its d (and dmin), the tokens' dx and (Q4_K) the min term -I2
+    float ep_d[2], ep_dm[2];
+    f32x4 ep_dx[2][4];
+    v16f ep_cm[2];
+    v8h ep_am[2], ep_bm[2];
+    auto epi_read = [&](const ScaleBuf& S, int nt) {
+        ep_d[nt] = S.d[nrow[nt]];
+#pragma unroll
+        for (int q = 0; q < 4; q++) ep_dx[nt][q] = *reinterpret_cast<const f32x4*>(&S.dx[32 * wave + 8 * q + 4 * half]);
+        if constexpr (TYPE == TYPE_Q4_K) {
+            ep_dm[nt] = S.dm[nrow[nt]];
+            ep_bm[nt] = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&S.wmin[nrow[nt] * GP_MROW + 4 * half]));
+            ep_am[nt] = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&S.xmin[(32 * wave + l32) * GP_MROW + 4 * half]));
+        }
+    };
+    // two outputs (2c, 2c+1) of pending tile nt, from its integer sums a
+    auto epi_part = [&](int nt, int c, const v16i& a) {
+#pragma unroll
+        for (int e = 2 * c; e < 2 * c + 2; e++) {
+            const float v = __fmul_rn(ep_d[nt], (float)a[e]);
+            if constexpr (TYPE == TYPE_Q4_K)
+                yacc[nt][e] = __builtin_fmaf(ep_dx[nt][e >> 2][e & 3], __builtin_fmaf(ep_dm[nt], ep_cm[nt][e], v), yacc[nt][e]);
+            else
+                yacc[nt][e] = __builtin_fmaf(ep_dx[nt][e >> 2][e & 3], v, yacc[nt][e]);
+        }
+    };
+
+    using SC = GpSched<TYPE>;
+    auto step = [&](auto p2_c, auto p3_c, int g) {
+        constexpr int p2 = decltype(p2_c)::value, p3 = decltype(p3_c)::value;
+        PlaneBuf& Lc = p2 ? LP1 : LP0;                  // planes of g (read)
+        PlaneBuf& Ln = p2 ? LP0 : LP1;                  // planes of g+1 (written)
+        ScaleBuf& Sn = p3 == 0 ? LS1 : p3 == 1 ? LS2 : LS0;   // scales of g+1 (written)
+        ScaleBuf& Sp = p3 == 0 ? LS2 : p3 == 1 ? LS0 : LS1;   // scales of g-1 (tile 1 epilogue)
+        ScaleBuf& Sc = p3 == 0 ? LS0 : p3 == 1 ? LS1 : LS2;   // scales of g (tile 0 epilogue)
+        const int gn = g + 1 < gend ? g + 1 : gend - 1;
+        const int g2 = g + 2 < gend ? g + 2 : gend - 1;
+
+        v16i& acc1 = acc1s[p2];                         // tile 1's sums of g
+        const v16i& acc1p = acc1s[p2 ^ 1];              // tile 1's sums of g-1 (epilogue pending)
+        constexpr int NB = KQ_GP_AHEAD + 1;
+        v4i bb[NB];                                     // B operands, read KQ_GP_AHEAD int8 MFMAs ahead
+        auto read_b = [&](int code, v4i& b) {
+            const int t = (code >> 3) & 1, ks = code & 7;
+            const int8_t* base = code < 16 ? Lc.wh : Lc.wl;
+            b = *reinterpret_cast<const v4i*>(base + prw(nrow[t], 2 * ks + half));
+        };
+        static_for<0, KQ_GP_AHEAD>([&](auto k) {
+            constexpr int code = gp_code_at<SC>(decltype(k)::value);
+            read_b(code, bb[decltype(k)::value]);
+        });
+
+        static_for<0, SC::NSLOT>([&](auto S) {
+            constexpr int s = decltype(S)::value;
+            // work chunks of this slot
+            static_for<0, UnpackP<TYPE>::NCHUNK>([&](auto c) {
+                if constexpr (SC::U[decltype(c)::value] == s) up.template chunk<decltype(c)::value>(raw, pi, prow, Ln, Sn);
+            });
+            if constexpr (SC::XS == s) stage_xp(rx, mr, xp, TYPE == TYPE_Q4_K, Sn);
+            if constexpr (SC::RAW == s) {
+                load_rawp(raw, wr, po, g2 * 8 * BS);
+                load_xp(rx, xr, xoff, xp, g2 * Q8K_BYTES);
+            }
+            static_for<0, 2>([&](auto t) {
+                constexpr int nt = decltype(t)::value;
+                v16i& acc = nt == 0 ? acc0 : acc1;
+                if constexpr (SC::ER[nt] == s) epi_read(nt == 0 ? Sc : Sp, nt);
+                static_for<0, 8>([&](auto c) {
+                    if constexpr (SC::E[nt][decltype(c)::value] == s)
+                        epi_part(nt, decltype(c)::value, nt == 0 ? acc0 : acc1p);
+                });
+                if constexpr (SC::SH[nt][0] == s) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[e] <<= SHIFT;
+                }
+                if constexpr (SC::SH[nt][1] == s) {
+#pragma unroll
+                    for (int e = 8; e < 16; e++) acc[e] <<= SHIFT;
+                }
+            });
+            // the slot's MFMA
+            constexpr int code = SC::mf[s];
+#if KQ_GP_PRIO
+            __builtin_amdgcn_s_setprio(KQ_GP_PRIO);
+#endif
+            if constexpr (code < 32) {
+                constexpr int t = (code >> 3) & 1, ks = code & 7, pos = gp_pos<SC>(s);
+                const bool first = code < 16 && ks == 0;
+                v16i& acc = t == 0 ? acc0 : acc1;
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[ks], bb[pos % NB], first ? v16i{} : acc, 0, 0, 0);
+                constexpr int nxt = gp_code_at<SC>(pos + KQ_GP_AHEAD);
+                if constexpr (nxt >= 0) read_b(nxt, bb[(pos + KQ_GP_AHEAD) % NB]);
+            } else if constexpr (TYPE == TYPE_Q4_K) {
+                ep_cm[code - 32] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ep_am[code - 32], ep_bm[code - 32], v16f{}, 0, 0, 0);
+            }
+#if KQ_GP_PRIO
+            __builtin_amdgcn_s_setprio(0);
+#endif
+            static_for<0, 8>([&](auto k) {
+                constexpr int ks = decltype(k)::value;
+                if constexpr (SC::A[ks] == s)
+                    afr[ks] = load_a(ks, gn);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        __syncthreads();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    for (int g = gbeg; g < gend; g += 6) {
+        step(I0{}, I0{}, g);
+        if (g + 1 < gend) step(I1{}, I1{}, g + 1);
+        if (g + 2 < gend) step(I0{}, I2{}, g + 2);
+        if (g + 3 < gend) step(I1{}, I0{}, g + 3);
+        if (g + 4 < gend) step(I0{}, I1{}, g + 4);
+        if (g + 5 < gend) step(I1{}, I2{}, g + 5);
+    }
+    // tile 1's epilogue of the last super-block
+    {
+        const int p3 = (gend - 1 - gbeg) % 3;
+        const ScaleBuf& S = p3 == 0 ? LS0 : p3 == 1 ? LS1 : LS2;
+        auto last = [&](const v16i& a) {
+            epi_read(S, 1);
+            if constexpr (TYPE == TYPE_Q4_K)
+                ep_cm[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ep_am[1], ep_bm[1], v16f{}, 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < 8; c++) epi_part(1, c, a);
+        };
+        if ((gend - 1 - gbeg) & 1) last(acc1s[1]);
+        else last(acc1s[0]);
+    }
+
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        const int n = n0 + nrow[nt];
+#pragma unroll
+        for (int a = 0; a < 16; a++) {
+            const int m = m0 + 32 * wave + (a >> 2) * 8 + half * 4 + (a & 3);
+            if (m < M && n < R) Yo[(int64_t)m * ldo + n] = yacc[nt][a];
+        }
+    }
+}
 
 // Fragment-order copy of the activation quants (layout above); rows M .. 256*ceil(M/256)-1 are
 // zero.  One workgroup per (32-row tile, super-block), 32 bytes per thread.
@@ -544,12 +1057,13 @@ k_gemm_reduce(ReduceGroup rg, int M) {
     *reinterpret_cast<f32x4_a4*>(Y + (int64_t)m * ldy + r) = a;
 }
 
-// Tiles of the launch below: 64 weight rows x 128 tokens.
+// Tiles of the K-split rule: 64 weight rows x 128 tokens, and the workgroups that fill the GPU: two
+// per CU of the 256 on an MI355X (fixed, so the split and the workspace size do not depend on the
+// device or on the kernel a call runs).  The pipelined kernel's 64 x 256 tiles at one workgroup per
+// CU give the same S whenever M is a multiple of 256.  Measured (two-wave kernel, us, unsplit ->
+// split): 4096x12288 Q6_K at M = 32 / 64 / 128 / 256 / 512: 91.7 / 93.4 / 98.4 / 99.9 / 103.2 ->
+// 34.6 / 35.9 / 38.1 / 57.8 / 96.1; 12288x4096 Q4_K at M = 32 / 64: 33.6 / 33.5 -> 31.5 / 33.0.
 constexpr int GM_TN = 64, GM_TM = 128;
-// Workgroups that fill the GPU: two per CU of the 256 on an MI355X (fixed, so the split and the
-// workspace size do not depend on the device).  Measured (us, unsplit -> split): 4096x12288 Q6_K
-// at M = 32 / 64 / 128 / 256 / 512: 91.7 / 93.4 / 98.4 / 99.9 / 103.2 -> 34.6 / 35.9 / 38.1 /
-// 57.8 / 96.1; 12288x4096 Q4_K at M = 32 / 64: 33.6 / 33.5 -> 31.5 / 33.0.
 constexpr int GM_FILL = 512;
 constexpr int GM_SPLIT_MIN = 4;     // super-blocks per split, at least
 #ifndef KQ_GEMM_SPLIT_MAX
@@ -593,17 +1107,8 @@ size_t gemm_q8k_group_workspace(int n, const int* R, int C, int M) {
 
 size_t gemm_q8k_workspace(int R, int C, int M) { return gemm_q8k_group_workspace(1, &R, C, M); }
 
-template <int TYPE, int BN, int WN, int WM, int MT>
-static void launch_tile(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, const uint8_t* xf, int M,
-                        const int* S, hipStream_t s) {
-    constexpr int BM = 32 * MT * WM;
-    static_assert(BN == GM_TN && BM == GM_TM, "the split rule assumes these tiles");
-    dim3 grid(wgs, (M + BM - 1) / BM), block(64 * WN * WM);
-    if (xf)
-        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, true, MT>), grid, block, 0, s, gg, G, xq, xf, M);
-    else
-        hipLaunchKernelGGL((k_gemm_q8k<TYPE, BN, WN, WM, false, MT>), grid, block, 0, s, gg, G, xq, xf, M);
-    // one reduce launch for the matrices that split K
+// One reduce launch for the matrices of a group that split K.
+static void launch_reduce(const GemmGroup& gg, int M, const int* S, hipStream_t s) {
     ReduceGroup rg{};
     int blks = 0;
     for (int i = 0; i < gg.n; i++) {
@@ -621,17 +1126,41 @@ static void launch_tile(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, 
     if (rg.n) hipLaunchKernelGGL(k_gemm_reduce, dim3(blks), dim3(256), 0, s, rg, M);
 }
 
+// Which kernel runs a launch.  The pipelined kernel (256 tokens x 64 rows, one 8-wave workgroup per
+// CU) serves Q6_K from 129 tokens: its shared unpack halves the heavy Q6_K plane arithmetic per
+// output (4096x12288 at M = 256 / 512 / 2048: 53.6 / 89.1 / 298 -> 47.1 / 77.2 / 259 us).  Q4_K
+// stays on the two-wave kernel: with the min term's operands the pipelined kernel needs more than
+// 256 registers and spills (12288x4096 at M = 512 / 2048: 77 / 287 -> 94 / 307 us).  Its raw buffer
+// descriptors address at most 2^31 bytes per buffer.
+static bool use_pipelined(int type, int R, int C, int M) {
+    const int64_t G = C / QK;
+    return type == TYPE_Q6_K && M > 128 && (int64_t)R * G * Q6K_BYTES < (int64_t(1) << 31) &&
+           (int64_t)((M + GP_BM - 1) / GP_BM * GP_BM) * G * Q8K_BYTES < (int64_t(1) << 31);
+}
+
 template <int TYPE>
 static void launch_type(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, const uint8_t* xf, int M,
-                        const int* S, hipStream_t s) {
-    // 128 tokens x 64 weight rows per workgroup of 4 waves (80 KB of LDS, at most 256 VGPRs), so two
-    // workgroups share a CU and each SIMD holds two waves: one wave's unpack and epilogue run under
-    // the other's MFMAs.  Each wave takes 32 tokens x all 64 rows (MT = 1): half the A-operand
-    // loads of 64 tokens x 32 rows (MT = 2), for twice the B reads from LDS; 12288x4096 Q4_K at
-    // M = 2048 / 512 / 256: 285 / 76.8 / 49.3 -> 270 / 73.8 / 45.7 us, 4096x12288 Q6_K 311 / 91.2
-    // -> 300 / 88.1 us.  (Measured against 128 x 128 tiles, one wave per SIMD, 4-8 waves per
-    // workgroup: 289-317 against 331-379 us at M = 2048.)
-    launch_tile<TYPE, 64, 1, 4, 1>(gg, wgs, G, xq, xf, M, S, s);
+                        const int* S, bool pipelined, hipStream_t s) {
+    if (pipelined) {
+        dim3 grid(wgs, (M + GP_BM - 1) / GP_BM), block(GP_THREADS);
+        if (xf)
+            hipLaunchKernelGGL((k_gemm_q8k_p<TYPE, true>), grid, block, 0, s, gg, G, xq, xf, M);
+        else
+            hipLaunchKernelGGL((k_gemm_q8k_p<TYPE, false>), grid, block, 0, s, gg, G, xq, xf, M);
+    } else {
+        // 128 tokens x 64 weight rows per workgroup of 4 waves (80 KB of LDS, at most 256 VGPRs), so
+        // two workgroups share a CU and each SIMD holds two waves: one wave's unpack and epilogue run
+        // under the other's MFMAs.  Each wave takes 32 tokens x all 64 rows (MT = 1): half the A-operand
+        // loads of 64 tokens x 32 rows (MT = 2), for twice the B reads from LDS; 12288x4096 Q4_K at
+        // M = 2048 / 512 / 256: 285 / 76.8 / 49.3 -> 270 / 73.8 / 45.7 us, 4096x12288 Q6_K 311 / 91.2
+        // -> 300 / 88.1 us.
+        dim3 grid(wgs, (M + GM_TM - 1) / GM_TM), block(256);
+        if (xf)
+            hipLaunchKernelGGL((k_gemm_q8k<TYPE, GM_TN, 1, 4, true, 1>), grid, block, 0, s, gg, G, xq, xf, M);
+        else
+            hipLaunchKernelGGL((k_gemm_q8k<TYPE, GM_TN, 1, 4, false, 1>), grid, block, 0, s, gg, G, xq, xf, M);
+    }
+    launch_reduce(gg, M, S, s);
 }
 
 // ------------------------------------------------------------------ the no-allocation form
@@ -715,8 +1244,10 @@ void launch_gemm_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
             gg.n++;
         }
         if (!gg.n) continue;
-        if (ty == TYPE_Q4_K) launch_type<TYPE_Q4_K>(gg, wgs, G, xq, ws, M, Sg, s);
-        else launch_type<TYPE_Q6_K>(gg, wgs, G, xq, ws, M, Sg, s);
+        bool pipelined = true;
+        for (int i = 0; i < gg.n; i++) pipelined = pipelined && use_pipelined(ty, gg.m[i].R, C, M);
+        if (ty == TYPE_Q4_K) launch_type<TYPE_Q4_K>(gg, wgs, G, xq, ws, M, Sg, pipelined, s);
+        else launch_type<TYPE_Q6_K>(gg, wgs, G, xq, ws, M, Sg, pipelined, s);
     }
 }
 

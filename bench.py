@@ -351,6 +351,33 @@ def batched_extra(torch, rn, dev, steps):
     return out
 
 
+def single_gemv_extra(torch, rn, dev, copies=64, reps=8):
+    """One 4096x4096 Q4_K GEMV at batch 1 (seed-0 N(0, 0.02) weights, one N(0, 1) activation row):
+    the GEMV alone on a resident Q8_K row, and with the row's quantization in front of it.  64
+    resident weight copies (605 MB) rotate so the 256 MB last-level cache cannot serve repeats; each
+    graph holds one call per copy."""
+    from kq import quantize as kqq
+    R = C_ = 4096
+    base = torch.from_numpy(kqq.synthetic_matrix(R, C_, 12, seed=0)).to(dev)
+    ws = [base] + [base.clone() for _ in range(copies - 1)]
+    x = torch.from_numpy(kqq.synthetic_activations(1, C_, seed=0)[0]).to(dev)
+    xq = torch.empty((C_ // 256) * Q8K, dtype=torch.uint8, device=dev)
+    y = torch.empty(R, device=dev)
+    rn.quantize(x, C_, xq, rn.stream())
+    out = {}
+    gemv_bytes = wbytes(R, C_, 12) + (C_ // 256) * Q8K + R * 4
+    for name, fn, nbytes in (
+            ("gemv", lambda s, w: rn.gemv(w, R, C_, 12, xq, 1, y, s), gemv_bytes),
+            ("quantize_gemv", lambda s, w: (rn.quantize(x, C_, xq, s), rn.gemv(w, R, C_, 12, xq, 1, y, s)),
+             gemv_bytes + C_ * 4 + (C_ // 256) * Q8K)):
+        g = capture(torch, lambda: [fn(rn.stream(), w) for w in ws])
+        time_graphs(torch, [g] * 2)
+        per = time_graphs(torch, [g] * reps) / (reps * copies)
+        out[name] = {"us": round(per * 1e6, 2), "GB/s": round(nbytes / per / 1e9, 1),
+                     "hbm_frac": round(nbytes / per / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    return out
+
+
 def verify_layer_extra(torch, rn, layers, dev, steps=320):
     """Speculative verify of N draft tokens through one decode layer's 7 matrices (the batched form of
     the step: Engine.gemv_batch's path; the ternary engine's spec.verify, spec.py:790): each of the 4
@@ -793,7 +820,8 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
-    ap.add_argument("--only", choices=("batched", "verify", "producers", "f32_layer", "gemm", "head", "decode_stream",
+    ap.add_argument("--only", choices=("single", "batched", "verify", "producers", "f32_layer", "gemm", "head",
+                                       "decode_stream",
                                        "pack", "tp_shard", "prefill_chunk"),
                     help="run only this extra (no headline step, no CPU baseline) and print its JSON; for "
                          "profiling one workload")
@@ -823,7 +851,8 @@ def main():
     if a.only:
         need_layers = a.only in ("verify", "producers", "f32_layer", "prefill_chunk")
         lay = make_layer(torch, dev, a.copies) if need_layers else None
-        fn = {"batched": lambda: batched_extra(torch, rn, dev, 160),
+        fn = {"single": lambda: single_gemv_extra(torch, rn, dev),
+              "batched": lambda: batched_extra(torch, rn, dev, 160),
               "verify": lambda: verify_layer_extra(torch, rn, lay, dev),
               "producers": lambda: producers_extra(torch, rn, lay, dev),
               "f32_layer": lambda: f32_layer_extra(torch, rn, lay, dev),
@@ -895,6 +924,8 @@ def main():
                      "avg_bytes_per_launch": round(kb), "avg_us_per_launch": round(ks * 1e6, 3)},
     }
     if not a.no_extras:
+        log("bench: single 4096x4096 Q4_K GEMV")
+        result["single_gemv_4096"] = single_gemv_extra(torch, rn, dev)
         log("bench: batched GEMV")
         result["batched_gemv"] = batched_extra(torch, rn, dev, 160)
         log("bench: speculative verify through a layer")

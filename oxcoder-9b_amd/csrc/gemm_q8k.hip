@@ -865,8 +865,6 @@ k_gemm_q8k_p(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t*
     v8h ep_am[2], ep_bm[2];
     auto epi_read = [&](const ScaleBuf& S, int nt) {
         ep_d[nt] = S.d[nrow[nt]];
-#pragma unroll
-        for (int q = 0; q < 4; q++) ep_dx[nt][q] = *reinterpret_cast<const f32x4*>(&S.dx[32 * wave + 8 * q + 4 * half]);
         if constexpr (TYPE == TYPE_Q4_K) {
             ep_dm[nt] = S.dm[nrow[nt]];
             ep_bm[nt] = __builtin_bit_cast(v8h, *reinterpret_cast<const u32x4*>(&S.wmin[nrow[nt] * GP_MROW + 4 * half]));
@@ -925,6 +923,14 @@ k_gemm_q8k_p(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t*
                 constexpr int nt = decltype(t)::value;
                 v16i& acc = nt == 0 ? acc0 : acc1;
                 if constexpr (SC::ER[nt] == s) epi_read(nt == 0 ? Sc : Sp, nt);
+                // the tokens' dx, one 4-vector per two chunks, read one chunk ahead of its first use (all
+                // 16 held at once cost 12 registers more and made the Q4_K form spill)
+                static_for<0, 4>([&](auto q) {
+                    constexpr int qq = decltype(q)::value;
+                    constexpr int at = qq == 0 ? SC::ER[nt] : SC::E[nt][2 * qq - 1];
+                    if constexpr (at == s)
+                        ep_dx[nt][qq] = *reinterpret_cast<const f32x4*>(&(nt == 0 ? Sc : Sp).dx[32 * wave + 8 * qq + 4 * half]);
+                });
                 static_for<0, 8>([&](auto c) {
                     if constexpr (SC::E[nt][decltype(c)::value] == s)
                         epi_part(nt, decltype(c)::value, nt == 0 ? acc0 : acc1p);
@@ -982,6 +988,8 @@ k_gemm_q8k_p(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t*
         const ScaleBuf& S = p3 == 0 ? LS0 : p3 == 1 ? LS1 : LS2;
         auto last = [&](const v16i& a) {
             epi_read(S, 1);
+#pragma unroll
+            for (int q = 0; q < 4; q++) ep_dx[1][q] = *reinterpret_cast<const f32x4*>(&S.dx[32 * wave + 8 * q + 4 * half]);
             if constexpr (TYPE == TYPE_Q4_K)
                 ep_cm[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ep_am[1], ep_bm[1], v16f{}, 0, 0, 0);
 #pragma unroll
@@ -1129,9 +1137,9 @@ static void launch_reduce(const GemmGroup& gg, int M, const int* S, hipStream_t 
 // Which kernel runs a launch.  The pipelined kernel (256 tokens x 64 rows, one 8-wave workgroup per
 // CU) serves Q6_K from 129 tokens: its shared unpack halves the heavy Q6_K plane arithmetic per
 // output (4096x12288 at M = 256 / 512 / 2048: 53.6 / 89.1 / 298 -> 47.1 / 77.2 / 259 us).  Q4_K
-// stays on the two-wave kernel: with the min term's operands the pipelined kernel needs more than
-// 256 registers and spills (12288x4096 at M = 512 / 2048: 77 / 287 -> 94 / 307 us).  Its raw buffer
-// descriptors address at most 2^31 bytes per buffer.
+// stays on the two-wave kernel, which the pipelined one does not beat for it (12288x4096 at M = 256
+// / 512 / 2048: 46.0 / 73.9 / 269-277 against 44.9 / 85.0 / 276 us).  The pipelined kernel's raw
+// buffer descriptors address at most 2^31 bytes per buffer.
 static bool use_pipelined(int type, int R, int C, int M) {
     const int64_t G = C / QK;
     return type == TYPE_Q6_K && M > 128 && (int64_t)R * G * Q6K_BYTES < (int64_t(1) << 31) &&
@@ -1141,13 +1149,18 @@ static bool use_pipelined(int type, int R, int C, int M) {
 template <int TYPE>
 static void launch_type(const GemmGroup& gg, int wgs, int G, const uint8_t* xq, const uint8_t* xf, int M,
                         const int* S, bool pipelined, hipStream_t s) {
-    if (pipelined) {
-        dim3 grid(wgs, (M + GP_BM - 1) / GP_BM), block(GP_THREADS);
-        if (xf)
-            hipLaunchKernelGGL((k_gemm_q8k_p<TYPE, true>), grid, block, 0, s, gg, G, xq, xf, M);
-        else
-            hipLaunchKernelGGL((k_gemm_q8k_p<TYPE, false>), grid, block, 0, s, gg, G, xq, xf, M);
-    } else {
+    if constexpr (TYPE == TYPE_Q6_K) {          // (the Q4_K form is not dispatched: see use_pipelined)
+        if (pipelined) {
+            dim3 grid(wgs, (M + GP_BM - 1) / GP_BM), block(GP_THREADS);
+            if (xf)
+                hipLaunchKernelGGL((k_gemm_q8k_p<TYPE, true>), grid, block, 0, s, gg, G, xq, xf, M);
+            else
+                hipLaunchKernelGGL((k_gemm_q8k_p<TYPE, false>), grid, block, 0, s, gg, G, xq, xf, M);
+            launch_reduce(gg, M, S, s);
+            return;
+        }
+    }
+    {
         // 128 tokens x 64 weight rows per workgroup of 4 waves (80 KB of LDS, at most 256 VGPRs), so
         // two workgroups share a CU and each SIMD holds two waves: one wave's unpack and epilogue run
         // under the other's MFMAs.  Each wave takes 32 tokens x all 64 rows (MT = 1): half the A-operand

@@ -41,6 +41,9 @@ typedef short s16x2 __attribute__((ext_vector_type(2)));
 #ifndef KQ_GEMV_MFMA_Q6_PLANES
 #define KQ_GEMV_MFMA_Q6_PLANES 0   // 1: Q6_K through the two-plane form instead of sub-block phases
 #endif
+#ifndef KQ_GEMV_MFMA_RG
+#define KQ_GEMV_MFMA_RG 1          // plane form with at most 32 super-blocks: two row groups per wave
+#endif
 #ifndef KQ_GEMV_MFMA_Q4_PH_MAX
 #define KQ_GEMV_MFMA_Q4_PH_MAX 4   // Q4_K through the phase form up to this many tokens (at most 8)
 #endif
@@ -574,6 +577,104 @@ k_gemv_mfma_ph(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     mv_merge(part, nchunks, G, N, R, row0, mg.y[m], mg.ldy[m]);
 }
 
+// ------------------------------------------------------------------ two row groups per wave
+// The plane form with each wave on two 16-row groups x two super-blocks (a "piece": half a chunk)
+// instead of one group x four: the same waves and MFMAs, but each activation operand (16 tokens x 256
+// bytes per super-block, more than the weights it meets from 5 tokens on) is loaded once for 32 rows,
+// so a launch loads half the activation bytes.  A workgroup holds 32 rows and every piece of them
+// (ceil(G/2) <= 16 waves, so G <= 32); each wave adds its two super-block values (v0 + v1) or (v2 + v3)
+// and the merge forms each chunk as (v0 + v1) + (v2 + v3) before the pass tree, so every output is the
+// one k_gemv_mfma (and the one-token GEMV) gives.
+constexpr int MV_ROWS2 = 32;    // weight rows per workgroup of the two-group form
+
+template <int TYPE, int LB>
+__global__ void __launch_bounds__(LB)
+k_gemv_mfma_rg(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
+    constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    __shared__ float part[16][16][MV_ROWS2];           // [piece][token][row] piece sums
+    const int lane = threadIdx.x & 63;
+    const int piece = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int npieces = blockDim.x >> 6;
+    const int q = lane >> 4, l16 = lane & 15;
+
+    const int wg = blockIdx.x;
+    const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
+    const int R = mg.R[m];
+    const int row0 = (wg - mg.first[m]) * MV_ROWS2;
+    const int64_t col_bytes = 8 * BS;
+    const uint8_t* wrow[2];
+#pragma unroll
+    for (int rg = 0; rg < 2; rg++) {
+        int row = row0 + 16 * rg + l16;
+        row = row < R ? row : R - 1;                   // rows past R are loaded clamped, not stored
+        wrow[rg] = mg.w[m] + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
+    }
+    const int64_t xrow = (int64_t)G * Q8K_BYTES;
+    const uint8_t* xa = XQ + (int64_t)(l16 < N ? l16 : N - 1) * xrow;
+    const uint8_t* xd[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = 4 * q + j;
+        xd[j] = XQ + (int64_t)(n < N ? n : N - 1) * xrow;
+    }
+
+    // the piece's two super-blocks, every load issued before the first is used; columns past G are
+    // loaded clamped and contribute +0
+    const int g0 = 2 * piece;
+    MvW<TYPE> w[2][2];
+    MvX x[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int g = g0 + s < G ? g0 + s : G - 1;
+#pragma unroll
+        for (int rg = 0; rg < 2; rg++) mv_load(w[s][rg], wrow[rg] + (int64_t)g * col_bytes, q);
+        const uint8_t* xdg[4] = {xd[0] + g * Q8K_BYTES, xd[1] + g * Q8K_BYTES, xd[2] + g * Q8K_BYTES,
+                                 xd[3] + g * Q8K_BYTES};
+        mv_load_x<TYPE>(x[s], xa + (int64_t)g * Q8K_BYTES, xdg, q);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float v[2][2][4];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const bool valid = g0 + s < G;
+#pragma unroll
+        for (int rg = 0; rg < 2; rg++) {
+            float vv[4];
+            mv_values(w[s][rg], x[s], q, vv);
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[rg][s][j] = valid ? vv[j] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int rg = 0; rg < 2; rg++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) part[piece][4 * q + j][16 * rg + l16] = __fadd_rn(v[rg][0][j], v[rg][1][j]);
+    __syncthreads();
+
+    // merge: thread (token n, row r); chunk c = pieces 2c, 2c + 1, passes of 4 chunks, missing ones +0
+    const int passes = (G + 15) / 16;
+    float* const y = mg.y[m];
+    const int64_t ldy = mg.ldy[m];
+    for (int idx = threadIdx.x; idx < N * MV_ROWS2; idx += blockDim.x) {
+        const int n = idx / MV_ROWS2, r = idx - n * MV_ROWS2;
+        if (row0 + r >= R) continue;
+        PassTree tr;
+        tree_init(tr);
+        for (int ps = 0; ps < passes; ps++) {
+            float c[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int p0 = 2 * (4 * ps + k);
+                const float a = p0 < npieces ? part[p0][n][r] : 0.0f;
+                const float b = p0 + 1 < npieces ? part[p0 + 1][n][r] : 0.0f;
+                c[k] = __fadd_rn(a, b);
+            }
+            tree_push(tr, __fadd_rn(__fadd_rn(c[0], c[1]), __fadd_rn(c[2], c[3])));
+        }
+        y[(int64_t)n * ldy + row0 + r] = tree_final(tr);
+    }
+}
+
 template <int TYPE, int LB, bool PRE_ALL, bool SB>
 static void launch_mv(const MvGroup& mg, int wgs, const uint8_t* xq, int N, int G, hipStream_t s) {
     const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
@@ -590,8 +691,10 @@ static void launch_mv(const MvGroup& mg, int wgs, const uint8_t* xq, int N, int 
 //   Q6_K up to 8 tokens and 48 super-blocks: the phase form, all four super-blocks in flight for
 //   up to 4 tokens, two for 5..8 (4096x12288 at N = 3 / 4 / 5 / 8: 15.3 / 15.3 / 15.3 / 16.1 ->
 //   12.7 / 12.8 / 14.0 / 14.4 us; 4096x4096 at N = 4: 7.0 -> 5.9 us);
-//   otherwise the plane form: Q4_K with G <= 16 all four super-blocks in flight (3 waves per SIMD),
-//   else two in flight, behind the barrier.
+//   otherwise the plane form: with G <= 32 (Q4_K) or G <= 16 (Q6_K) two row groups per wave
+//   (k_gemv_mfma_rg: 12288x4096 Q4_K at N = 16 13.9-14.1 -> 12.8 us, N = 8 unchanged); beyond, Q4_K
+//   with G <= 16 all four super-blocks in flight (3 waves per SIMD), else two in flight, behind the
+//   barrier.
 void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
                             int N, float* const* y, const int64_t* ldy, hipStream_t s) {
     const int G = C / QK;
@@ -618,6 +721,23 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
     } else if (ph) {
         if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q6_K, 1, 768, KQ_Q6P_FP1>), grid, block, 0, s, mg, xq, N, G);
         else hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q6_K, 2, 768, KQ_Q6P_FP2>), grid, block, 0, s, mg, xq, N, G);
+    } else if (KQ_GEMV_MFMA_RG && G <= (type == TYPE_Q4_K ? 32 : 16)) {
+        // two row groups per wave: workgroups of 32 rows (Q6_K beyond 16 super-blocks, 4 waves per SIMD,
+        // would spill)
+        MvGroup mg2 = mg;
+        int wgs2 = 0;
+        for (int i = 0; i < n; i++) {
+            mg2.first[i] = wgs2;
+            wgs2 += (R[i] + MV_ROWS2 - 1) / MV_ROWS2;
+        }
+        for (int i = n; i < 4; i++) mg2.first[i] = wgs2;
+        const dim3 block2(64 * ((G + 1) / 2));
+        if (type == TYPE_Q4_K) {
+            if (G <= 16) hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q4_K, 512>), dim3(wgs2), block2, 0, s, mg2, xq, N, G);
+            else hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q4_K, 1024>), dim3(wgs2), block2, 0, s, mg2, xq, N, G);
+        } else {
+            hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q6_K, 512>), dim3(wgs2), block2, 0, s, mg2, xq, N, G);
+        }
     } else if (type == TYPE_Q4_K) {
         if (G <= 16) launch_mv<TYPE_Q4_K, 256, true, true>(mg, wgs, xq, N, G, s);
         else if (G <= 48) launch_mv<TYPE_Q4_K, 768, false, true>(mg, wgs, xq, N, G, s);

@@ -170,6 +170,7 @@ def test_gemv_q8k_reference_inputs(dev, orc, ty):
     (12, 1000, 4096),                                       # Q4_K below it: v_dot4 to 3 tokens, then MFMA
     (12, 4096, 8448), (14, 4096, 12032),                    # G = 33 / 47: a last chunk of 1 / 3 super-blocks
     (14, 4096, 16384), (12, 4104, 14336),                   # G = 64 / 56 on many rows: the plane form's 16 / 14 waves
+    (12, 136, 7936), (14, 4104, 3840),                      # two-group plane form: G = 31 / 15 (a half-empty last piece)
 ])
 def test_batched_rows_bit_identical_to_single(dev, orc, ty, R, C):
     """Speculative-verify invariant: every row of a batch equals its N = 1 result bit for bit."""
@@ -234,7 +235,7 @@ def test_batched_reference_inputs_bit_identical(dev, orc, ty):
     assert_close_inf(host(yb), orc.gemv_q8k(W, R, C, ty, xq, 7))
 
 
-@pytest.mark.parametrize("C,N", [(4096, 1), (4096, 3), (4096, 6), (12288, 2), (12288, 4)])
+@pytest.mark.parametrize("C,N", [(4096, 1), (4096, 3), (4096, 6), (4096, 16), (12288, 2), (12288, 4)])
 def test_gemv_q8k_multi_matches_single(dev, orc, C, N):
     """q/k/v-style group (two Q4_K, one Q6_K) in one call equals three single calls bit for bit; at
     C = 12288 and two tokens the Q4_K matrices take the MFMA kernel and the Q6_K one the v_dot4 GEMV

@@ -48,6 +48,27 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, kq_expf(-g))), u);
 }
 
+// Lane t + N's value of v in lane t, for the lanes t < N of a halving step within a wave: the gfx950
+// permlane swaps for N = 32, 16 (the second result holds rows 1 and 3, halves 1), DPP row_shl for
+// N = 8 .. 1 (lane t <- lane t + N within its row of 16).  Lanes t >= N receive values no step uses.
+template <int N>
+__device__ __forceinline__ double lane_plus(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+    uint32_t a, b;
+    if constexpr (N == 32) {
+        a = xor32_pair(lo).b;
+        b = xor32_pair(hi).b;
+    } else if constexpr (N == 16) {
+        a = xor16_pair(lo).b;
+        b = xor16_pair(hi).b;
+    } else {
+        a = (uint32_t)dpp<0x100 + N>((int)lo);
+        b = (uint32_t)dpp<0x100 + N>((int)hi);
+    }
+    return __builtin_bit_cast(double, ((uint64_t)b << 32) | a);
+}
+
 // One workgroup per row: 16 waves, or 8 when J > 32 (16 would leave 128 VGPRs per thread for the J
 // row values and spill).  Threads 0..255 do the first pass (J >= D/256 row elements each, a
 // compile-time count, so every load is unconditional: elements past D re-read element D-1 and are
@@ -65,6 +86,7 @@ k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int 
     constexpr int B = (J + RMS_WAVES - 1) / RMS_WAVES;   // Q8_K blocks per wave, at most
     extern __shared__ float hrow[];            // D floats
     __shared__ double sums[128];
+    __shared__ double sums64[64];
     __shared__ float s_sh;
     const int t = threadIdx.x, row = blockIdx.x;
     const int lane = t & 63, wv = t >> 6;
@@ -105,21 +127,32 @@ k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int 
             }
         }
     }
-    // the halving tree of q4.cu:42-43: sums[t] += sums[t + n] for n = 128, 64, ..., 1
+    // the halving tree of q4.cu:42-43: sums[t] += sums[t + n] for n = 128, 64, ..., 1; the n = 64
+    // level has its own array (no barrier between its stores and the n = 128 reads), and n = 32 .. 1
+    // run in wave 0's registers
     if (t >= 128 && t < 256) sums[t - 128] = sum;
     __syncthreads();
-    if (t < 128) sum = __dadd_rn(sum, sums[t]);                 // n = 128
-    __syncthreads();
-    if (t >= 64 && t < 128) sums[t - 64] = sum;
+    if (t < 128) {
+        sum = __dadd_rn(sum, sums[t]);                           // n = 128
+        if (t >= 64) sums64[t - 64] = sum;
+    }
     __syncthreads();
     if (t < 64) {
-        sum = __dadd_rn(sum, sums[t]);                           // n = 64
-#pragma unroll
-        for (int n = 32; n; n >>= 1) sum = __dadd_rn(sum, __shfl_down(sum, n, 64));   // lane t += lane t + n
+        sum = __dadd_rn(sum, sums64[t]);                         // n = 64
+        sum = __dadd_rn(sum, lane_plus<32>(sum));                // lane t += lane t + n
+        sum = __dadd_rn(sum, lane_plus<16>(sum));
+        sum = __dadd_rn(sum, lane_plus<8>(sum));
+        sum = __dadd_rn(sum, lane_plus<4>(sum));
+        sum = __dadd_rn(sum, lane_plus<2>(sum));
+        sum = __dadd_rn(sum, lane_plus<1>(sum));
         if (t == 0) {
             // sqrtf correctly rounded: the double square root of a float, rounded to float, is
             // (53 >= 2*24 + 2 bits), while v_sqrt_f32 alone is not
-            const float ms = __fadd_rn((float)__ddiv_rn(sum, (double)D), 1e-6f);
+            // sum / D; for D = 2^k the product with 2^-k is the same double, without a division
+            const double mean = (D & (D - 1)) == 0
+                ? __dmul_rn(sum, __builtin_bit_cast(double, (uint64_t)(1023 - __builtin_ctz((unsigned)D)) << 52))
+                : __ddiv_rn(sum, (double)D);
+            const float ms = __fadd_rn((float)mean, 1e-6f);
             s_sh = __fdiv_rn(1.0f, (float)__dsqrt_rn((double)ms));
         }
     }

@@ -505,9 +505,6 @@ constexpr int GP_BM = 256, GP_BN = 64, GP_THREADS = 512;
 #ifndef KQ_GP_AHEAD
 #define KQ_GP_AHEAD 2       // B operands are read this many int8 MFMAs ahead of their use
 #endif
-#ifndef KQ_GP_PRIO
-#define KQ_GP_PRIO 0        // wave priority while issuing each MFMA (0: unchanged)
-#endif
 
 // Plane rows are padded to 272 B (68 dwords): consecutive rows start 4 banks apart, so the 16-byte
 // reads of 16 consecutive rows fall on distinct banks, and every address is the row's base plus an
@@ -946,9 +943,6 @@ k_gemm_q8k_p(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t*
             });
             // the slot's MFMA
             constexpr int code = SC::mf[s];
-#if KQ_GP_PRIO
-            __builtin_amdgcn_s_setprio(KQ_GP_PRIO);
-#endif
             if constexpr (code < 32) {
                 constexpr int t = (code >> 3) & 1, ks = code & 7, pos = gp_pos<SC>(s);
                 const bool first = code < 16 && ks == 0;
@@ -959,9 +953,6 @@ k_gemm_q8k_p(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t*
             } else if constexpr (TYPE == TYPE_Q4_K) {
                 ep_cm[code - 32] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ep_am[code - 32], ep_bm[code - 32], v16f{}, 0, 0, 0);
             }
-#if KQ_GP_PRIO
-            __builtin_amdgcn_s_setprio(0);
-#endif
             static_for<0, 8>([&](auto k) {
                 constexpr int ks = decltype(k)::value;
                 if constexpr (SC::A[ks] == s)

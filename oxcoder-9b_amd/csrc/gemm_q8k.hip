@@ -295,6 +295,28 @@ struct GemmGroup {
     int n;
 };
 
+// Kernel entry of the GEMM launches: every field of the three matrix records (and the other scalar
+// arguments) read in one batch of loads with one wait, each passing through an empty instruction
+// with the workgroup index, so that the matrix picked by that index takes its fields by selects over
+// values already in registers.  Left to the compiler, the prologue made four dependent round trips
+// of ~0.3 us to the kernel arguments (the field of the selected matrix was reloaded from a computed
+// address).  Pointers pass as integers and come back as global pointers (kq_global).
+#define KQ_GEMM_ARGS(gg)                                                                              \
+    int bx = blockIdx.x;                                                                              \
+    int64_t w0_ = (int64_t)(gg).m[0].w, w1_ = (int64_t)(gg).m[1].w, w2_ = (int64_t)(gg).m[2].w;      \
+    int64_t y0_ = (int64_t)(gg).m[0].y, y1_ = (int64_t)(gg).m[1].y, y2_ = (int64_t)(gg).m[2].y;      \
+    int64_t p0_ = (int64_t)(gg).m[0].part, p1_ = (int64_t)(gg).m[1].part, p2_ = (int64_t)(gg).m[2].part; \
+    int64_t l0_ = (gg).m[0].ldy, l1_ = (gg).m[1].ldy, l2_ = (gg).m[2].ldy;                           \
+    int R0_ = (gg).m[0].R, R1_ = (gg).m[1].R, R2_ = (gg).m[2].R;                                      \
+    int nt0_ = (gg).m[0].ntile, nt1_ = (gg).m[1].ntile, nt2_ = (gg).m[2].ntile;                       \
+    int gp0_ = (gg).m[0].gps, gp1_ = (gg).m[1].gps, gp2_ = (gg).m[2].gps;                             \
+    int wg1_ = (gg).m[1].wg0, wg2_ = (gg).m[2].wg0, nmat = (gg).n;                                    \
+    asm volatile("" : "+s"(bx), "+s"(w0_), "+s"(w1_), "+s"(w2_), "+s"(y0_), "+s"(y1_), "+s"(y2_), "+s"(p0_), \
+                 "+s"(p1_), "+s"(p2_), "+s"(l0_), "+s"(l1_), "+s"(l2_), "+s"(R0_), "+s"(R1_), "+s"(R2_),      \
+                 "+s"(nt0_), "+s"(nt1_), "+s"(nt2_), "+s"(gp0_), "+s"(gp1_), "+s"(gp2_), "+s"(wg1_), "+s"(wg2_), \
+                 "+s"(nmat) : "s"(G), "s"(XQ), "s"(XF), "s"(M));                                     \
+    __builtin_amdgcn_sched_barrier(0)
+
 // WN waves along n times WM along m; each wave owns MT token tiles x NT = 2/MT weight-row tiles of
 // 32x32 (two MFMA tiles), the workgroup BM = 32*MT*WM tokens x BN = 32*NT*WN rows.  With MT = 1 a wave
 // holds one token tile's A operands (32 VGPRs for a super-block) and uses each for both row tiles,
@@ -320,17 +342,17 @@ k_gemm_q8k(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t* _
     const int wm = wave % WM, wn = wave / WM;
     const int half = lane >> 5, l32 = lane & 31;
     // this workgroup's matrix (the argument fields picked by selects on the wave-uniform index)
-    const int bx = blockIdx.x;
-    const int mi = gg.n > 1 && bx >= gg.m[1].wg0 ? (gg.n > 2 && bx >= gg.m[2].wg0 ? 2 : 1) : 0;
-    auto field = [&](auto get) { return mi == 0 ? get(gg.m[0]) : mi == 1 ? get(gg.m[1]) : get(gg.m[2]); };
-    const uint8_t* const W = field([](const GemmMat& g) { return g.w; });
-    float* const Y = field([](const GemmMat& g) { return g.y; });
-    float* const P = field([](const GemmMat& g) { return g.part; });
-    const int64_t ldy = field([](const GemmMat& g) { return g.ldy; });
-    const int R = field([](const GemmMat& g) { return g.R; });
-    const int ntile = field([](const GemmMat& g) { return g.ntile; });
-    const int gps = field([](const GemmMat& g) { return g.gps; });
-    const int local = bx - field([](const GemmMat& g) { return g.wg0; });
+    KQ_GEMM_ARGS(gg);
+    const int mi = nmat > 1 && bx >= wg1_ ? (nmat > 2 && bx >= wg2_ ? 2 : 1) : 0;
+    auto pick = [&](auto a, auto b, auto c) { return mi == 0 ? a : mi == 1 ? b : c; };
+    const uint8_t* const W = kq_global<const uint8_t>(pick(w0_, w1_, w2_));
+    float* const Y = kq_global<float>(pick(y0_, y1_, y2_));
+    float* const P = kq_global<float>(pick(p0_, p1_, p2_));
+    const int64_t ldy = pick(l0_, l1_, l2_);
+    const int R = pick(R0_, R1_, R2_);
+    const int ntile = pick(nt0_, nt1_, nt2_);
+    const int gps = pick(gp0_, gp1_, gp2_);
+    const int local = bx - pick(0, wg1_, wg2_);
     const int split = local / ntile;
     const int n0 = (local - split * ntile) * BN, m0 = blockIdx.y * BM;
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
@@ -775,17 +797,17 @@ k_gemm_q8k_p(GemmGroup gg, int G, const uint8_t* __restrict__ XQ, const uint8_t*
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int half = lane >> 5, l32 = lane & 31;
-    const int bx = blockIdx.x;
-    const int mi = gg.n > 1 && bx >= gg.m[1].wg0 ? (gg.n > 2 && bx >= gg.m[2].wg0 ? 2 : 1) : 0;
-    auto field = [&](auto get) { return mi == 0 ? get(gg.m[0]) : mi == 1 ? get(gg.m[1]) : get(gg.m[2]); };
-    const uint8_t* const W = field([](const GemmMat& g) { return g.w; });
-    float* const Y = field([](const GemmMat& g) { return g.y; });
-    float* const P = field([](const GemmMat& g) { return g.part; });
-    const int64_t ldy = field([](const GemmMat& g) { return g.ldy; });
-    const int R = field([](const GemmMat& g) { return g.R; });
-    const int ntile = field([](const GemmMat& g) { return g.ntile; });
-    const int gps = field([](const GemmMat& g) { return g.gps; });
-    const int local = bx - field([](const GemmMat& g) { return g.wg0; });
+    KQ_GEMM_ARGS(gg);
+    const int mi = nmat > 1 && bx >= wg1_ ? (nmat > 2 && bx >= wg2_ ? 2 : 1) : 0;
+    auto pick = [&](auto a, auto b, auto c) { return mi == 0 ? a : mi == 1 ? b : c; };
+    const uint8_t* const W = kq_global<const uint8_t>(pick(w0_, w1_, w2_));
+    float* const Y = kq_global<float>(pick(y0_, y1_, y2_));
+    float* const P = kq_global<float>(pick(p0_, p1_, p2_));
+    const int64_t ldy = pick(l0_, l1_, l2_);
+    const int R = pick(R0_, R1_, R2_);
+    const int ntile = pick(nt0_, nt1_, nt2_);
+    const int gps = pick(gp0_, gp1_, gp2_);
+    const int local = bx - pick(0, wg1_, wg2_);
     const int split = local / ntile;
     const int n0 = (local - split * ntile) * GP_BN, m0 = blockIdx.y * GP_BM;
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
@@ -1034,16 +1056,26 @@ struct ReduceGroup {
 
 __global__ void __launch_bounds__(256)
 k_gemm_reduce(ReduceGroup rg, int M) {
-    const int bx = blockIdx.x;
-    const int j = rg.n > 1 && bx >= rg.m[1].blk0 ? (rg.n > 2 && bx >= rg.m[2].blk0 ? 2 : 1) : 0;
-    auto field = [&](auto get) { return j == 0 ? get(rg.m[0]) : j == 1 ? get(rg.m[1]) : get(rg.m[2]); };
-    const float* const P = field([](const ReduceMat& g) { return g.part; });
-    float* const Y = field([](const ReduceMat& g) { return g.y; });
-    const int64_t ldy = field([](const ReduceMat& g) { return g.ldy; });
-    const int R = field([](const ReduceMat& g) { return g.R; });
-    const int S = field([](const ReduceMat& g) { return g.S; });
+    // every argument in one batch of loads (one wait; see KQ_GEMM_ARGS)
+    int bx = blockIdx.x;
+    int64_t p0_ = (int64_t)rg.m[0].part, p1_ = (int64_t)rg.m[1].part, p2_ = (int64_t)rg.m[2].part;
+    int64_t y0_ = (int64_t)rg.m[0].y, y1_ = (int64_t)rg.m[1].y, y2_ = (int64_t)rg.m[2].y;
+    int64_t l0_ = rg.m[0].ldy, l1_ = rg.m[1].ldy, l2_ = rg.m[2].ldy;
+    int R0_ = rg.m[0].R, R1_ = rg.m[1].R, R2_ = rg.m[2].R, S0_ = rg.m[0].S, S1_ = rg.m[1].S, S2_ = rg.m[2].S;
+    int b1_ = rg.m[1].blk0, b2_ = rg.m[2].blk0, nmat = rg.n;
+    asm volatile("" : "+s"(bx), "+s"(p0_), "+s"(p1_), "+s"(p2_), "+s"(y0_), "+s"(y1_), "+s"(y2_), "+s"(l0_),
+                 "+s"(l1_), "+s"(l2_), "+s"(R0_), "+s"(R1_), "+s"(R2_), "+s"(S0_), "+s"(S1_), "+s"(S2_), "+s"(b1_),
+                 "+s"(b2_), "+s"(nmat) : "s"(M));
+    __builtin_amdgcn_sched_barrier(0);
+    const int j = nmat > 1 && bx >= b1_ ? (nmat > 2 && bx >= b2_ ? 2 : 1) : 0;
+    auto pick = [&](auto a, auto b, auto c) { return j == 0 ? a : j == 1 ? b : c; };
+    const float* const P = kq_global<const float>(pick(p0_, p1_, p2_));
+    float* const Y = kq_global<float>(pick(y0_, y1_, y2_));
+    const int64_t ldy = pick(l0_, l1_, l2_);
+    const int R = pick(R0_, R1_, R2_);
+    const int S = pick(S0_, S1_, S2_);
     const int r4 = R >> 2;
-    const int64_t i = (int64_t)(bx - field([](const ReduceMat& g) { return g.blk0; })) * 256 + threadIdx.x;
+    const int64_t i = (int64_t)(bx - pick(0, b1_, b2_)) * 256 + threadIdx.x;
     if (i >= (int64_t)M * r4) return;
     const int64_t pstride = (int64_t)M * R;
     const int m = (int)(i / r4), r = (int)(i - (int64_t)m * r4) * 4;

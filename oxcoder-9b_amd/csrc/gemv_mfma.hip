@@ -70,6 +70,19 @@ struct MvGroup {
     int R[3];
     int first[4];   // workgroups of matrix m are [first[m], first[m+1])
 };
+// Kernel entry: every field of the matrix table (and the other scalar arguments) read in one batch,
+// then matrix m's fields picked by selects rather than indexed loads that would wait for m.
+// The workgroup index goes through the same empty instruction, so nothing that selects by it (the
+// matrix and its fields) is placed ahead of the batch.
+#define KQ_MV_ARGS(mg, wg, ...)                                                                       \
+    do {                                                                                              \
+        asm volatile("" : "+s"(wg) : "s"((mg).w[0]), "s"((mg).w[1]), "s"((mg).w[2]), "s"((mg).y[0]),  \
+                     "s"((mg).y[1]), "s"((mg).y[2]), "s"((mg).ldy[0]), "s"((mg).ldy[1]), "s"((mg).ldy[2]), \
+                     "s"((mg).R[0]), "s"((mg).R[1]), "s"((mg).R[2]), "s"((mg).first[1]), "s"((mg).first[2]), \
+                     __VA_ARGS__);                                                                    \
+        __builtin_amdgcn_sched_barrier(0);                                                            \
+    } while (0)
+template <class T> __device__ __forceinline__ T mv_pick(int m, T a, T b, T c) { return m == 0 ? a : m == 1 ? b : c; }
 
 __device__ __forceinline__ uint32_t mv_mul_u8x4(uint32_t q, uint32_t s2) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * __builtin_bit_cast(u16x2, s2));
@@ -253,21 +266,24 @@ __device__ __forceinline__ void mv_merge(const float (*part)[16][MV_ROWS], int n
 template <int TYPE, int LB, bool PRE_ALL, bool SB>
 __global__ void __launch_bounds__(LB)
 k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
+    const int nthr = 64 * ((G + MV_CHUNK - 1) / MV_CHUNK);   // the block: one wave per chunk
+    int wg = blockIdx.x;
+    KQ_MV_ARGS(mg, wg, "s"(XQ), "s"(N), "s"(G), "s"(nthr));
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float part[16][16][MV_ROWS];            // [chunk][token][row] chunk sums
     const int lane = threadIdx.x & 63;
     const int chunk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nchunks = blockDim.x >> 6;
+    const int nchunks = nthr >> 6;
     const int q = lane >> 4, l16 = lane & 15;
 
-    const int wg = blockIdx.x;
     const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
-    const int R = mg.R[m];
-    const int row0 = (wg - mg.first[m]) * MV_ROWS;
+    const int R = mv_pick(m, mg.R[0], mg.R[1], mg.R[2]);
+    const int row0 = (wg - mv_pick(m, 0, mg.first[1], mg.first[2])) * MV_ROWS;
+    const uint8_t* const wm = mv_pick(m, mg.w[0], mg.w[1], mg.w[2]);
     int row = row0 + l16;
     row = row < R ? row : R - 1;                       // rows past R are loaded clamped, not stored
     const int64_t col_bytes = 8 * BS;
-    const uint8_t* wrow = mg.w[m] + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
+    const uint8_t* wrow = wm + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
     const uint8_t* xa = XQ + (int64_t)(l16 < N ? l16 : N - 1) * xrow;
     const uint8_t* xd[4];
@@ -327,7 +343,7 @@ k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     __syncthreads();
 
     // merge: thread (token n, row r); passes of 4 chunks, missing chunks are +0
-    mv_merge(part, nchunks, G, N, R, row0, mg.y[m], mg.ldy[m]);
+    mv_merge(part, nchunks, G, N, R, row0, mv_pick(m, mg.y[0], mg.y[1], mg.y[2]), mv_pick(m, mg.ldy[0], mg.ldy[1], mg.ldy[2]));
 }
 
 // ------------------------------------------------------------------ the phase form (no planes)
@@ -510,22 +526,25 @@ __device__ __forceinline__ void buf_ld(u32x2& v, __amdgpu_buffer_rsrc_t r, int o
 template <int TYPE, int NG, int LB, int FP>
 __global__ void __launch_bounds__(LB)
 k_gemv_mfma_ph(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
+    const int nthr = 64 * ((G + MV_CHUNK - 1) / MV_CHUNK);   // the block: one wave per chunk
+    int wg = blockIdx.x;
+    KQ_MV_ARGS(mg, wg, "s"(XQ), "s"(N), "s"(G), "s"(nthr));
     typedef MvPh<TYPE> Ph;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float part[16][16][MV_ROWS];            // [chunk][token][row] chunk sums
     const int lane = threadIdx.x & 63;
     const int chunk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nchunks = blockDim.x >> 6;
+    const int nchunks = nthr >> 6;
     const int q = lane >> 4, l16 = lane & 15;
 
-    const int wg = blockIdx.x;
     const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
-    const int R = mg.R[m];
-    const int row0 = (wg - mg.first[m]) * MV_ROWS;
+    const int R = mv_pick(m, mg.R[0], mg.R[1], mg.R[2]);
+    const int row0 = (wg - mv_pick(m, 0, mg.first[1], mg.first[2])) * MV_ROWS;
+    const uint8_t* const wm = mv_pick(m, mg.w[0], mg.w[1], mg.w[2]);
     int row = row0 + l16;
     row = row < R ? row : R - 1;                       // rows past R are loaded clamped, not stored
     const int64_t col_bytes = 8 * BS;
-    const uint8_t* wrow = mg.w[m] + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
+    const uint8_t* wrow = wm + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
     const int xrow = G * Q8K_BYTES;
     // raw buffer over the N activation rows: stride 0, N * xrow bytes (loads past them return 0), and
     // the gfx9 descriptor word 3 (32-bit data format)
@@ -574,7 +593,7 @@ k_gemv_mfma_ph(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
         part[chunk][4 * gi + q][l16] = __fadd_rn(__fadd_rn(v[0][gi], v[1][gi]), __fadd_rn(v[2][gi], v[3][gi]));
     __syncthreads();
 
-    mv_merge(part, nchunks, G, N, R, row0, mg.y[m], mg.ldy[m]);
+    mv_merge(part, nchunks, G, N, R, row0, mv_pick(m, mg.y[0], mg.y[1], mg.y[2]), mv_pick(m, mg.ldy[0], mg.ldy[1], mg.ldy[2]));
 }
 
 // ------------------------------------------------------------------ two row groups per wave
@@ -590,24 +609,27 @@ constexpr int MV_ROWS2 = 32;    // weight rows per workgroup of the two-group fo
 template <int TYPE, int LB>
 __global__ void __launch_bounds__(LB)
 k_gemv_mfma_rg(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
+    const int nthr = 64 * ((G + 1) / 2);                     // the block: one wave per piece
+    int wg = blockIdx.x;
+    KQ_MV_ARGS(mg, wg, "s"(XQ), "s"(N), "s"(G), "s"(nthr));
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float part[16][16][MV_ROWS2];           // [piece][token][row] piece sums
     const int lane = threadIdx.x & 63;
     const int piece = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int npieces = blockDim.x >> 6;
+    const int npieces = nthr >> 6;
     const int q = lane >> 4, l16 = lane & 15;
 
-    const int wg = blockIdx.x;
     const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
-    const int R = mg.R[m];
-    const int row0 = (wg - mg.first[m]) * MV_ROWS2;
+    const int R = mv_pick(m, mg.R[0], mg.R[1], mg.R[2]);
+    const int row0 = (wg - mv_pick(m, 0, mg.first[1], mg.first[2])) * MV_ROWS2;
+    const uint8_t* const wm = mv_pick(m, mg.w[0], mg.w[1], mg.w[2]);
     const int64_t col_bytes = 8 * BS;
     const uint8_t* wrow[2];
 #pragma unroll
     for (int rg = 0; rg < 2; rg++) {
         int row = row0 + 16 * rg + l16;
         row = row < R ? row : R - 1;                   // rows past R are loaded clamped, not stored
-        wrow[rg] = mg.w[m] + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
+        wrow[rg] = wm + ((int64_t)(row >> 3) * G * 8 + (row & 7)) * BS;   // + g * col_bytes
     }
     const int64_t xrow = (int64_t)G * Q8K_BYTES;
     const uint8_t* xa = XQ + (int64_t)(l16 < N ? l16 : N - 1) * xrow;
@@ -653,9 +675,9 @@ k_gemv_mfma_rg(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
 
     // merge: thread (token n, row r); chunk c = pieces 2c, 2c + 1, passes of 4 chunks, missing ones +0
     const int passes = (G + 15) / 16;
-    float* const y = mg.y[m];
-    const int64_t ldy = mg.ldy[m];
-    for (int idx = threadIdx.x; idx < N * MV_ROWS2; idx += blockDim.x) {
+    float* const y = mv_pick(m, mg.y[0], mg.y[1], mg.y[2]);
+    const int64_t ldy = mv_pick(m, mg.ldy[0], mg.ldy[1], mg.ldy[2]);
+    for (int idx = threadIdx.x; idx < N * MV_ROWS2; idx += nthr) {
         const int n = idx / MV_ROWS2, r = idx - n * MV_ROWS2;
         if (row0 + r >= R) continue;
         PassTree tr;

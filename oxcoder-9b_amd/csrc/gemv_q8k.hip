@@ -72,6 +72,29 @@ struct MatGroup {
     int n;
 };
 
+// The matrix table as scalars (w0..w2, y0..y2, l0..l2, f1, f2), with matrix m's fields picked by
+// selects.  A kernel declares them at entry and passes them, with its other scalar arguments, through
+// KQ_ARGS_READY, so that all its argument loads are issued before the first wait: left to the
+// compiler, each load sank to its first use, and the prologue made three or four dependent round
+// trips of ~0.3 us to the kernel arguments before its first weight load (a per-wave timeline of the
+// 4096x12288 Q6_K GEMV: arguments read 0.9 us after the wave's first instruction), an indexed read
+// of w[m] waiting for m.  (Kept in a struct with selecting member functions, the table went to
+// scratch memory instead.)
+#define KQ_MATS(mg)                                                                                   \
+    const uint8_t* const w0 = (mg).w[0];                                                              \
+    const uint8_t* const w1 = (mg).w[1];                                                              \
+    const uint8_t* const w2 = (mg).w[2];                                                              \
+    float* const y0 = (mg).y[0];                                                                      \
+    float* const y1 = (mg).y[1];                                                                      \
+    float* const y2 = (mg).y[2];                                                                      \
+    const int64_t l0 = (mg).ldy[0], l1 = (mg).ldy[1], l2 = (mg).ldy[2];                               \
+    const int f1 = (mg).first_unit[1], f2 = (mg).first_unit[2];                                       \
+    auto mat_of = [&](int u) { return u >= f1 ? (u >= f2 ? 2 : 1) : 0; };                             \
+    auto first_of = [&](int m) { return m == 0 ? 0 : m == 1 ? f1 : f2; };                             \
+    auto w_of = [&](int m) { return m == 0 ? w0 : m == 1 ? w1 : w2; };                                \
+    auto y_of = [&](int m) { return m == 0 ? y0 : m == 1 ? y1 : y2; };                                \
+    auto ldy_of = [&](int m) { return m == 0 ? l0 : m == 1 ? l1 : l2; }
+
 // Unit order of a wave (stream s of S streams in workgroup b of nwg; units of one 8-row tile:
 // WPT).  With S >= WPT the streams of a workgroup hold whole tiles when numbered consecutively:
 // unit = b*S + s + k*nwg*S.  With S < WPT (one-row Q6_K units over 4 streams, or several column
@@ -375,10 +398,13 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
     // Logical workgroup index grouped by die: workgroups are dealt to the XCDs in turn, so the
     // consecutive logical indices b, b + 1, whose streams share an 8-row tile (and the 128-byte lines
     // its rows' blocks straddle), run behind one L2 (4096x12288 Q6_K: 10.6 -> 10.4 us).
+    KQ_MATS(mg);
+    const int ngrid = gridDim.x, nthr = blockDim.x;
+    KQ_ARGS_READY("s"(w0), "s"(w1), "s"(w2), "s"(y0), "s"(y1), "s"(y2), "s"(l0), "s"(l1), "s"(l2), "s"(f1), "s"(f2),
+                  "s"(XQ), "s"(G), "s"(total_units), "s"(ngrid), "s"(nthr));
     int lwg = blockIdx.x;
-    if (gridDim.x % KQ_XCDS == 0) lwg = (lwg % KQ_XCDS) * (gridDim.x / KQ_XCDS) + lwg / KQ_XCDS;
-    const TileWalk<WPT, false> walk{lwg, (int)gridDim.x, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
-                                    (int)(blockDim.x >> 6)};
+    if (ngrid % KQ_XCDS == 0) lwg = (lwg % KQ_XCDS) * (ngrid / KQ_XCDS) + lwg / KQ_XCDS;
+    const TileWalk<WPT, false> walk{lwg, ngrid, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nthr >> 6};
     int u = walk.first();
     if (u >= total_units) return;
     const int p = lane & 3, slot = lane >> 2;
@@ -388,6 +414,17 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
 
     // Unit -> (matrix, first row) and the row-block address.  The unit index is wave-uniform,
     // so the argument-struct reads below are scalar loads and never wait on the weight stream.
+    // (the first unit's from the registers of the prologue's batch; later units' from the argument
+    // table, whose scalar loads the streaming loop hides: selects there made the loop's control flow
+    // branchier and its wait for the current unit a wait for every load, 89 -> 96 us on a 510 MB head)
+    auto unit_base0 = [&](int uu, int& m, int64_t& row0) -> const uint8_t* {
+        m = mat_of(uu);
+        const int v = uu - first_of(m);
+        const int64_t tile = v / WPT;
+        const int r0 = (v - (int)tile * WPT) * RPW;
+        row0 = tile * 8 + r0;
+        return w_of(m) + tile * tile_bytes + r0 * BS;
+    };
     auto unit_base = [&](int uu, int& m, int64_t& row0) -> const uint8_t* {
         m = uu >= mg.first_unit[1] ? (uu >= mg.first_unit[2] ? 2 : 1) : 0;
         const int v = uu - mg.first_unit[m];
@@ -419,7 +456,7 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
     Frag<TYPE> bufA[RPW], bufB[RPW];
     int m;
     int64_t row0;
-    const uint8_t* base = unit_base(u, m, row0);
+    const uint8_t* base = unit_base0(u, m, row0);
 #pragma unroll
     for (int r = 0; r < RPW; r++) load_frag(bufA[r], base + (int64_t)slot_c * col_bytes + r * BS, p);
     PassTree tree[NT][RPW];
@@ -598,13 +635,17 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
 // (argmax_block.h; aws is its workspace).
 template <int TYPE, int NT, int RPW, bool AMAX, class AP = ActQ8K>
 __global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
-k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units, int P, int kmax,
+k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units, int P, int K, int kmax,
                  uint8_t* aws, int* aout) {
     using ActT = typename AP::template A<TYPE>;
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     extern __shared__ float part[];                    // [stream][k][t][r][pass]
-    const int K = (blockDim.x >> 6) / P;               // unit streams per workgroup
+    // K: unit streams per workgroup (the block holds K * P waves)
+    KQ_MATS(mg);
+    const int ngrid = gridDim.x;
+    KQ_ARGS_READY("s"(w0), "s"(w1), "s"(w2), "s"(y0), "s"(y1), "s"(y2), "s"(l0), "s"(l1), "s"(l2), "s"(f1), "s"(f2),
+                  "s"(XQ), "s"(G), "s"(total_units), "s"(P), "s"(K), "s"(ngrid));
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pass = wave % P, stream = wave / P;
@@ -612,7 +653,7 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
     // that share cache lines (144- and 210-byte blocks do not align to 128-byte lines) are read by
     // one CU through one L2.  (Contiguous unit ranges per stream, with the streams of each XCD
     // grouped, were slower: gate+up 12.2 -> 13.1 us, the output head 95 -> 108 us.)
-    const int nwg = gridDim.x;
+    const int nwg = ngrid;
     const int lwg = blockIdx.x;
     const TileWalk<WPT> walk{lwg, nwg, stream, K};
     const int u_begin = walk.first(), u_end = total_units;
@@ -623,6 +664,16 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
     const bool valid = g < G;
     const int gc = valid ? g : G - 1;                  // lanes past the last column read column G-1, masked
 
+    // (the first unit's from the prologue's registers, later units' from the argument table: see
+    // k_gemv_q8k)
+    auto unit_base0 = [&](int uu, int& m, int64_t& row0) -> const uint8_t* {
+        m = mat_of(uu);
+        const int v = uu - first_of(m);
+        const int64_t tile = v / WPT;
+        const int r0 = (v - (int)tile * WPT) * RPW;
+        row0 = tile * 8 + r0;
+        return w_of(m) + tile * tile_bytes + r0 * BS + gc * col_bytes;
+    };
     auto unit_base = [&](int uu, int& m, int64_t& row0) -> const uint8_t* {
         m = uu >= mg.first_unit[1] ? (uu >= mg.first_unit[2] ? 2 : 1) : 0;
         const int v = uu - mg.first_unit[m];
@@ -641,7 +692,7 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
         Frag<TYPE> bufA[RPW], bufB[RPW];
         int u = u_begin, k = 0, m;
         int64_t row0;
-        const uint8_t* base = unit_base(u, m, row0);
+        const uint8_t* base = unit_base0(u, m, row0);
 #pragma unroll
         for (int r = 0; r < RPW; r++) load_frag(bufA[r], base + r * BS, p);
         float* mypart = part + (int64_t)stream * kmax * NT * RPW * P;
@@ -691,7 +742,7 @@ k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_u
         const TileWalk<WPT> ws{lwg, nwg, st, K};
         const int nk = ws.count(total_units);
         const float* sp = part + (int64_t)st * kmax * NT * RPW * P;
-        for (int idx = threadIdx.x; idx < nk * NT * RPW; idx += blockDim.x) {
+        for (int idx = threadIdx.x; idx < nk * NT * RPW; idx += 64 * K * P) {
             const int kk = idx / (NT * RPW), t = (idx / RPW) % NT, r = idx % RPW;
             const int uu = ws.unit(kk);
             const int mm = uu >= mg.first_unit[1] ? (uu >= mg.first_unit[2] ? 2 : 1) : 0;
@@ -762,7 +813,7 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
             }
         }
         hipLaunchKernelGGL((k_gemv_q8k_split<TYPE, NT, RPW, AMAX, AP>), dim3(nwg), dim3(64 * passes * K), lds, s, mg,
-                           xq, G, total, passes, kmax, aws, aout);
+                           xq, G, total, passes, K, kmax, aws, aout);
         return;
     }
     const int wpb = KQ_GEMV_SEQ_WPB;

@@ -132,6 +132,28 @@ __device__ __forceinline__ float xor32_max(float v) {
     return __builtin_fmaxf(__builtin_bit_cast(float, r.a), __builtin_bit_cast(float, r.b));
 }
 
+// An empty instruction that takes every listed kernel-argument value in scalar registers: the loads
+// that produce them are all issued ahead of it, and its wait is the kernel prologue's only one.  Left
+// to the compiler, each argument load sinks to its first use, and a prologue whose addresses depend on
+// earlier arguments (grid and block size, a matrix table indexed by the wave's matrix) makes several
+// dependent round trips of ~0.3 us to the kernel arguments before its first data load.  Each value
+// keeps a use besides the later ones, so selects over them are not folded back into an indexed load,
+// and pointers keep their global address space (as outputs of the instruction they would not).  The
+// scheduling barrier keeps later work from being hoisted above it (and waiting on part of the batch).
+#define KQ_ARGS_READY(...)                                                                            \
+    do {                                                                                              \
+        asm volatile("" ::__VA_ARGS__);                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                            \
+    } while (0)
+
+// A pointer that passed through an empty instruction as an integer, as a global pointer again: the
+// cast through the global address space lets loads through it be global (not flat) loads.
+template <class T>
+__device__ __forceinline__ T* kq_global(int64_t v) {
+    typedef __attribute__((address_space(1))) T GT;
+    return (T*)(GT*)(uintptr_t)v;
+}
+
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
     return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);

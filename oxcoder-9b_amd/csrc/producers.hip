@@ -189,8 +189,10 @@ k_rms_q8k(float* h, const float* res, int add, const float* __restrict__ w, int 
 __global__ void __launch_bounds__(256)
 k_swiglu_q8k(const float* __restrict__ gate, const float* __restrict__ up, int G, int64_t ld, int nblocks,
              float* __restrict__ y, uint8_t* __restrict__ xq) {
+    const int nthr = blockDim.x;
+    KQ_ARGS_READY("s"(gate), "s"(up), "s"(G), "s"(ld), "s"(nblocks), "s"(y), "s"(xq), "s"(nthr));
     const int lane = threadIdx.x & 63;
-    const int blk = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int blk = blockIdx.x * (nthr >> 6) + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     const int n = blk / G, g = blk - n * G;
     const int64_t i0 = (int64_t)n * ld + (int64_t)g * QK + 4 * lane;

@@ -8,8 +8,11 @@ namespace kq {
 
 __global__ void __launch_bounds__(256)
 k_q8k_quantize(const float* __restrict__ x, int64_t ldx, int G, int nblocks, uint8_t* __restrict__ xq) {
+    // every argument load issued before the first wait (one round trip to the arguments, not two)
+    const int nthr = blockDim.x;
+    KQ_ARGS_READY("s"(x), "s"(ldx), "s"(G), "s"(nblocks), "s"(xq), "s"(nthr));
     const int lane = threadIdx.x & 63;
-    const int blk = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int blk = blockIdx.x * (nthr >> 6) + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     const int n = blk / G, g = blk - n * G;
     const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + (int64_t)n * ldx + (int64_t)g * QK + 4 * lane);
@@ -24,8 +27,10 @@ k_q8k_quantize(const float* __restrict__ x, int64_t ldx, int G, int nblocks, uin
 __global__ void __launch_bounds__(256)
 k_q8k_quantize_frag(const float* __restrict__ x, int64_t ldx, int G, int M, int nblocks, uint8_t* __restrict__ xq,
                     uint8_t* __restrict__ xf) {
+    const int nthr = blockDim.x;
+    KQ_ARGS_READY("s"(x), "s"(ldx), "s"(G), "s"(M), "s"(nblocks), "s"(xq), "s"(xf), "s"(nthr));
     const int lane = threadIdx.x & 63;
-    const int blk = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int blk = blockIdx.x * (nthr >> 6) + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     const int n = blk / G, g = blk - n * G;
     uint8_t* fo = xf + (((int64_t)(n >> 5) * G + g) * 8 + (lane >> 3)) * 1024 +

@@ -70,18 +70,21 @@ struct MvGroup {
     int R[3];
     int first[4];   // workgroups of matrix m are [first[m], first[m+1])
 };
-// Kernel entry: every field of the matrix table (and the other scalar arguments) read in one batch,
-// then matrix m's fields picked by selects rather than indexed loads that would wait for m.
-// The workgroup index goes through the same empty instruction, so nothing that selects by it (the
-// matrix and its fields) is placed ahead of the batch.
-#define KQ_MV_ARGS(mg, wg, ...)                                                                       \
-    do {                                                                                              \
-        asm volatile("" : "+s"(wg) : "s"((mg).w[0]), "s"((mg).w[1]), "s"((mg).w[2]), "s"((mg).y[0]),  \
-                     "s"((mg).y[1]), "s"((mg).y[2]), "s"((mg).ldy[0]), "s"((mg).ldy[1]), "s"((mg).ldy[2]), \
-                     "s"((mg).R[0]), "s"((mg).R[1]), "s"((mg).R[2]), "s"((mg).first[1]), "s"((mg).first[2]), \
-                     __VA_ARGS__);                                                                    \
-        __builtin_amdgcn_sched_barrier(0);                                                            \
-    } while (0)
+// Kernel arguments: first, as plain scalars, what the prologue needs (the three matrices' weights, the
+// activations, the row counts, the first workgroups of matrices 1 and 2 packed as f1 | f2 << 16, and
+// NxG = N | G << 8), 13 dwords that the dispatch preloads into scalar registers
+// (-amdgpu-kernarg-preload-count), so a wave's first loads wait for no argument fetch; the matrix table
+// follows for the outputs.  Matrix m's fields are picked by selects, not by an indexed load that would
+// wait for m.
+#define KQ_MV_HEAD                                                                                    \
+    const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const uint8_t* __restrict__ w2,   \
+        const uint8_t* __restrict__ XQ, int R0, int R1, int R2, int F12, int NxG
+#define KQ_MV_PICK(wg, rows)                                                                          \
+    const int N = NxG & 0xff, G = NxG >> 8;                                                           \
+    const int m = (wg) >= (F12 & 0xffff) ? ((wg) >= (F12 >> 16) ? 2 : 1) : 0;                         \
+    const int R = mv_pick(m, R0, R1, R2);                                                             \
+    const int row0 = ((wg) - mv_pick(m, 0, F12 & 0xffff, F12 >> 16)) * (rows);                        \
+    const uint8_t* const wm = mv_pick(m, w0, w1, w2)
 template <class T> __device__ __forceinline__ T mv_pick(int m, T a, T b, T c) { return m == 0 ? a : m == 1 ? b : c; }
 
 __device__ __forceinline__ uint32_t mv_mul_u8x4(uint32_t q, uint32_t s2) {
@@ -265,21 +268,17 @@ __device__ __forceinline__ void mv_merge(const float (*part)[16][MV_ROWS], int n
 // launch bound, which sets the register budget the compiler works to.
 template <int TYPE, int LB, bool PRE_ALL, bool SB>
 __global__ void __launch_bounds__(LB)
-k_gemv_mfma(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
-    const int nthr = 64 * ((G + MV_CHUNK - 1) / MV_CHUNK);   // the block: one wave per chunk
-    int wg = blockIdx.x;
-    KQ_MV_ARGS(mg, wg, "s"(XQ), "s"(N), "s"(G), "s"(nthr));
+k_gemv_mfma(KQ_MV_HEAD, MvGroup mg) {
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float part[16][16][MV_ROWS];            // [chunk][token][row] chunk sums
     const int lane = threadIdx.x & 63;
     const int chunk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nchunks = nthr >> 6;
     const int q = lane >> 4, l16 = lane & 15;
 
-    const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
-    const int R = mv_pick(m, mg.R[0], mg.R[1], mg.R[2]);
-    const int row0 = (wg - mv_pick(m, 0, mg.first[1], mg.first[2])) * MV_ROWS;
-    const uint8_t* const wm = mv_pick(m, mg.w[0], mg.w[1], mg.w[2]);
+    const int wg = blockIdx.x;
+    KQ_MV_PICK(wg, MV_ROWS);
+    const int nthr = 64 * ((G + MV_CHUNK - 1) / MV_CHUNK);   // the block: one wave per chunk
+    const int nchunks = nthr >> 6;
     int row = row0 + l16;
     row = row < R ? row : R - 1;                       // rows past R are loaded clamped, not stored
     const int64_t col_bytes = 8 * BS;
@@ -525,22 +524,18 @@ __device__ __forceinline__ void buf_ld(u32x2& v, __amdgpu_buffer_rsrc_t r, int o
 // the wave's four super-blocks are in flight before the first is used.
 template <int TYPE, int NG, int LB, int FP>
 __global__ void __launch_bounds__(LB)
-k_gemv_mfma_ph(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
-    const int nthr = 64 * ((G + MV_CHUNK - 1) / MV_CHUNK);   // the block: one wave per chunk
-    int wg = blockIdx.x;
-    KQ_MV_ARGS(mg, wg, "s"(XQ), "s"(N), "s"(G), "s"(nthr));
+k_gemv_mfma_ph(KQ_MV_HEAD, MvGroup mg) {
     typedef MvPh<TYPE> Ph;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float part[16][16][MV_ROWS];            // [chunk][token][row] chunk sums
     const int lane = threadIdx.x & 63;
     const int chunk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nchunks = nthr >> 6;
     const int q = lane >> 4, l16 = lane & 15;
 
-    const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
-    const int R = mv_pick(m, mg.R[0], mg.R[1], mg.R[2]);
-    const int row0 = (wg - mv_pick(m, 0, mg.first[1], mg.first[2])) * MV_ROWS;
-    const uint8_t* const wm = mv_pick(m, mg.w[0], mg.w[1], mg.w[2]);
+    const int wg = blockIdx.x;
+    KQ_MV_PICK(wg, MV_ROWS);
+    const int nthr = 64 * ((G + MV_CHUNK - 1) / MV_CHUNK);   // the block: one wave per chunk
+    const int nchunks = nthr >> 6;
     int row = row0 + l16;
     row = row < R ? row : R - 1;                       // rows past R are loaded clamped, not stored
     const int64_t col_bytes = 8 * BS;
@@ -608,21 +603,17 @@ constexpr int MV_ROWS2 = 32;    // weight rows per workgroup of the two-group fo
 
 template <int TYPE, int LB>
 __global__ void __launch_bounds__(LB)
-k_gemv_mfma_rg(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
-    const int nthr = 64 * ((G + 1) / 2);                     // the block: one wave per piece
-    int wg = blockIdx.x;
-    KQ_MV_ARGS(mg, wg, "s"(XQ), "s"(N), "s"(G), "s"(nthr));
+k_gemv_mfma_rg(KQ_MV_HEAD, MvGroup mg) {
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     __shared__ float part[16][16][MV_ROWS2];           // [piece][token][row] piece sums
     const int lane = threadIdx.x & 63;
     const int piece = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int npieces = nthr >> 6;
     const int q = lane >> 4, l16 = lane & 15;
 
-    const int m = wg >= mg.first[1] ? (wg >= mg.first[2] ? 2 : 1) : 0;
-    const int R = mv_pick(m, mg.R[0], mg.R[1], mg.R[2]);
-    const int row0 = (wg - mv_pick(m, 0, mg.first[1], mg.first[2])) * MV_ROWS2;
-    const uint8_t* const wm = mv_pick(m, mg.w[0], mg.w[1], mg.w[2]);
+    const int wg = blockIdx.x;
+    KQ_MV_PICK(wg, MV_ROWS2);
+    const int nthr = 64 * ((G + 1) / 2);                     // the block: one wave per piece
+    const int npieces = nthr >> 6;
     const int64_t col_bytes = 8 * BS;
     const uint8_t* wrow[2];
 #pragma unroll
@@ -697,11 +688,15 @@ k_gemv_mfma_rg(MvGroup mg, const uint8_t* __restrict__ XQ, int N, int G) {
     }
 }
 
+// The leading arguments of the MFMA kernels (KQ_MV_HEAD) from a group; the workgroup counts fit 16
+// bits (the dispatcher sends at most 65535 row groups to these forms).
+#define MV_HEAD_ARGS(g) (g).w[0], (g).w[1], (g).w[2], xq, (g).R[0], (g).R[1], (g).R[2], (g).first[1] | (g).first[2] << 16, N | G << 8
+
 template <int TYPE, int LB, bool PRE_ALL, bool SB>
 static void launch_mv(const MvGroup& mg, int wgs, const uint8_t* xq, int N, int G, hipStream_t s) {
     const int nchunks = (G + MV_CHUNK - 1) / MV_CHUNK;
-    hipLaunchKernelGGL((k_gemv_mfma<TYPE, LB, PRE_ALL, SB>), dim3(wgs), dim3(64 * nchunks), 0, s, mg, xq,
-                       N, G);
+    hipLaunchKernelGGL((k_gemv_mfma<TYPE, LB, PRE_ALL, SB>), dim3(wgs), dim3(64 * nchunks), 0, s, MV_HEAD_ARGS(mg),
+                       mg);
 }
 
 // n (1..3) matrices of one type, N = 1..16 tokens, C <= 16384 (at most 16 chunks of 4 columns).
@@ -738,11 +733,11 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
     // workgroup has 16 waves, 4 per SIMD (128 registers: spills too)
     const bool ph = G <= 48 && N <= 8 && (type == TYPE_Q4_K ? N <= KQ_GEMV_MFMA_Q4_PH_MAX : !KQ_GEMV_MFMA_Q6_PLANES);
     if (ph && type == TYPE_Q4_K) {
-        if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q4_K, 1, 768, KQ_Q4P_FP1>), grid, block, 0, s, mg, xq, N, G);
-        else hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q4_K, 2, 768, KQ_Q4P_FP2>), grid, block, 0, s, mg, xq, N, G);
+        if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q4_K, 1, 768, KQ_Q4P_FP1>), grid, block, 0, s, MV_HEAD_ARGS(mg), mg);
+        else hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q4_K, 2, 768, KQ_Q4P_FP2>), grid, block, 0, s, MV_HEAD_ARGS(mg), mg);
     } else if (ph) {
-        if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q6_K, 1, 768, KQ_Q6P_FP1>), grid, block, 0, s, mg, xq, N, G);
-        else hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q6_K, 2, 768, KQ_Q6P_FP2>), grid, block, 0, s, mg, xq, N, G);
+        if (N <= 4) hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q6_K, 1, 768, KQ_Q6P_FP1>), grid, block, 0, s, MV_HEAD_ARGS(mg), mg);
+        else hipLaunchKernelGGL((k_gemv_mfma_ph<TYPE_Q6_K, 2, 768, KQ_Q6P_FP2>), grid, block, 0, s, MV_HEAD_ARGS(mg), mg);
     } else if (KQ_GEMV_MFMA_RG && G <= (type == TYPE_Q4_K ? 32 : 16)) {
         // two row groups per wave: workgroups of 32 rows (Q6_K beyond 16 super-blocks, 4 waves per SIMD,
         // would spill)
@@ -755,10 +750,10 @@ void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C,
         for (int i = n; i < 4; i++) mg2.first[i] = wgs2;
         const dim3 block2(64 * ((G + 1) / 2));
         if (type == TYPE_Q4_K) {
-            if (G <= 16) hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q4_K, 512>), dim3(wgs2), block2, 0, s, mg2, xq, N, G);
-            else hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q4_K, 1024>), dim3(wgs2), block2, 0, s, mg2, xq, N, G);
+            if (G <= 16) hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q4_K, 512>), dim3(wgs2), block2, 0, s, MV_HEAD_ARGS(mg2), mg2);
+            else hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q4_K, 1024>), dim3(wgs2), block2, 0, s, MV_HEAD_ARGS(mg2), mg2);
         } else {
-            hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q6_K, 512>), dim3(wgs2), block2, 0, s, mg2, xq, N, G);
+            hipLaunchKernelGGL((k_gemv_mfma_rg<TYPE_Q6_K, 512>), dim3(wgs2), block2, 0, s, MV_HEAD_ARGS(mg2), mg2);
         }
     } else if (type == TYPE_Q4_K) {
         if (G <= 16) launch_mv<TYPE_Q4_K, 256, true, true>(mg, wgs, xq, N, G, s);

@@ -72,28 +72,22 @@ struct MatGroup {
     int n;
 };
 
-// The matrix table as scalars (w0..w2, y0..y2, l0..l2, f1, f2), with matrix m's fields picked by
-// selects.  A kernel declares them at entry and passes them, with its other scalar arguments, through
-// KQ_ARGS_READY, so that all its argument loads are issued before the first wait: left to the
-// compiler, each load sank to its first use, and the prologue made three or four dependent round
-// trips of ~0.3 us to the kernel arguments before its first weight load (a per-wave timeline of the
-// 4096x12288 Q6_K GEMV: arguments read 0.9 us after the wave's first instruction), an indexed read
-// of w[m] waiting for m.  (Kept in a struct with selecting member functions, the table went to
-// scratch memory instead.)
-#define KQ_MATS(mg)                                                                                   \
-    const uint8_t* const w0 = (mg).w[0];                                                              \
-    const uint8_t* const w1 = (mg).w[1];                                                              \
-    const uint8_t* const w2 = (mg).w[2];                                                              \
-    float* const y0 = (mg).y[0];                                                                      \
-    float* const y1 = (mg).y[1];                                                                      \
-    float* const y2 = (mg).y[2];                                                                      \
-    const int64_t l0 = (mg).ldy[0], l1 = (mg).ldy[1], l2 = (mg).ldy[2];                               \
-    const int f1 = (mg).first_unit[1], f2 = (mg).first_unit[2];                                       \
+// Kernel arguments.  The GEMV kernels take first, as plain scalars, what their prologue needs: the
+// three matrices' weights, the activations, G, the unit count, the first units of matrices 1 and 2,
+// the grid size and one more count, 14 dwords that the dispatch preloads into scalar registers
+// (-amdgpu-kernarg-preload-count; on firmware that does not preload, the code object's compatibility
+// prologue loads them in one batch).  The matrix table follows for the loop's later units and the
+// outputs.  The prologue picks the first unit's matrix by selects, not by an indexed load that would
+// wait for m.  (Left to the compiler with the table first, the prologue made three or four dependent
+// round trips of ~0.3 us to the kernel arguments before its first weight load: a per-wave timeline of
+// the 4096x12288 Q6_K GEMV read its arguments 0.9 us after the wave's first instruction.)
+#define KQ_GEMV_HEAD                                                                                  \
+    const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const uint8_t* __restrict__ w2,   \
+        const uint8_t* __restrict__ XQ, int G, int total_units, int f1, int f2, int ngrid
+#define KQ_GEMV_PICK                                                                                  \
     auto mat_of = [&](int u) { return u >= f1 ? (u >= f2 ? 2 : 1) : 0; };                             \
     auto first_of = [&](int m) { return m == 0 ? 0 : m == 1 ? f1 : f2; };                             \
-    auto w_of = [&](int m) { return m == 0 ? w0 : m == 1 ? w1 : w2; };                                \
-    auto y_of = [&](int m) { return m == 0 ? y0 : m == 1 ? y1 : y2; };                                \
-    auto ldy_of = [&](int m) { return m == 0 ? l0 : m == 1 ? l1 : l2; }
+    auto w_of = [&](int m) { return m == 0 ? w0 : m == 1 ? w1 : w2; }
 
 // Unit order of a wave (stream s of S streams in workgroup b of nwg; units of one 8-row tile:
 // WPT).  With S >= WPT the streams of a workgroup hold whole tiles when numbered consecutively:
@@ -389,7 +383,7 @@ struct ActF32 {
 // the step loop is unrolled over the passes so each step's pass is a compile-time index.
 template <int TYPE, int NT, int RPW, bool ONEPASS, int FP = 0, class AP = ActQ8K>
 __global__ void __launch_bounds__(256)
-k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) {
+k_gemv_q8k(KQ_GEMV_HEAD, int nwaves, MatGroup mg) {
     using ActT = typename AP::template A<TYPE>;
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
@@ -398,13 +392,11 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
     // Logical workgroup index grouped by die: workgroups are dealt to the XCDs in turn, so the
     // consecutive logical indices b, b + 1, whose streams share an 8-row tile (and the 128-byte lines
     // its rows' blocks straddle), run behind one L2 (4096x12288 Q6_K: 10.6 -> 10.4 us).
-    KQ_MATS(mg);
-    const int ngrid = gridDim.x, nthr = blockDim.x;
-    KQ_ARGS_READY("s"(w0), "s"(w1), "s"(w2), "s"(y0), "s"(y1), "s"(y2), "s"(l0), "s"(l1), "s"(l2), "s"(f1), "s"(f2),
-                  "s"(XQ), "s"(G), "s"(total_units), "s"(ngrid), "s"(nthr));
+    // nwaves: waves per workgroup
+    KQ_GEMV_PICK;
     int lwg = blockIdx.x;
     if (ngrid % KQ_XCDS == 0) lwg = (lwg % KQ_XCDS) * (ngrid / KQ_XCDS) + lwg / KQ_XCDS;
-    const TileWalk<WPT, false> walk{lwg, ngrid, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nthr >> 6};
+    const TileWalk<WPT, false> walk{lwg, ngrid, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nwaves};
     int u = walk.first();
     if (u >= total_units) return;
     const int p = lane & 3, slot = lane >> 2;
@@ -635,17 +627,14 @@ k_gemv_q8k(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units) 
 // (argmax_block.h; aws is its workspace).
 template <int TYPE, int NT, int RPW, bool AMAX, class AP = ActQ8K>
 __global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
-k_gemv_q8k_split(MatGroup mg, const uint8_t* __restrict__ XQ, int G, int total_units, int P, int K, int kmax,
-                 uint8_t* aws, int* aout) {
+k_gemv_q8k_split(KQ_GEMV_HEAD, int PK, MatGroup mg, int kmax, uint8_t* aws, int* aout) {
     using ActT = typename AP::template A<TYPE>;
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     extern __shared__ float part[];                    // [stream][k][t][r][pass]
-    // K: unit streams per workgroup (the block holds K * P waves)
-    KQ_MATS(mg);
-    const int ngrid = gridDim.x;
-    KQ_ARGS_READY("s"(w0), "s"(w1), "s"(w2), "s"(y0), "s"(y1), "s"(y2), "s"(l0), "s"(l1), "s"(l2), "s"(f1), "s"(f2),
-                  "s"(XQ), "s"(G), "s"(total_units), "s"(P), "s"(K), "s"(ngrid));
+    // PK = P | K << 8: P column passes, K unit streams per workgroup (the block holds K * P waves)
+    const int P = PK & 0xff, K = PK >> 8;
+    KQ_GEMV_PICK;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pass = wave % P, stream = wave / P;
@@ -812,8 +801,9 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
                 nwg = round_xcd(nwg * 2);
             }
         }
-        hipLaunchKernelGGL((k_gemv_q8k_split<TYPE, NT, RPW, AMAX, AP>), dim3(nwg), dim3(64 * passes * K), lds, s, mg,
-                           xq, G, total, passes, K, kmax, aws, aout);
+        hipLaunchKernelGGL((k_gemv_q8k_split<TYPE, NT, RPW, AMAX, AP>), dim3(nwg), dim3(64 * passes * K), lds, s,
+                           mg.w[0], mg.w[1], mg.w[2], xq, G, total, mg.first_unit[1], mg.first_unit[2], nwg,
+                           passes | K << 8, mg, kmax, aws, aout);
         return;
     }
     const int wpb = KQ_GEMV_SEQ_WPB;
@@ -822,14 +812,17 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
     dim3 grid((waves + wpb - 1) / wpb), block(64 * wpb);
     if constexpr (KQ_GEMV_P3 && NT <= 2 && RPW <= 2 && !AP::F32) {
         if (passes == 3) {
-            hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false, 3>), grid, block, 0, s, mg, xq, G, total);
+            hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false, 3>), grid, block, 0, s, mg.w[0], mg.w[1], mg.w[2], xq,
+                               G, total, mg.first_unit[1], mg.first_unit[2], (int)grid.x, wpb, mg);
             return;
         }
     }
     if (G <= 16)
-        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, true, 0, AP>), grid, block, 0, s, mg, xq, G, total);
+        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, true, 0, AP>), grid, block, 0, s, mg.w[0], mg.w[1], mg.w[2], xq,
+                           G, total, mg.first_unit[1], mg.first_unit[2], (int)grid.x, wpb, mg);
     else
-        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false, 0, AP>), grid, block, 0, s, mg, xq, G, total);
+        hipLaunchKernelGGL((k_gemv_q8k<TYPE, NT, RPW, false, 0, AP>), grid, block, 0, s, mg.w[0], mg.w[1], mg.w[2], xq,
+                           G, total, mg.first_unit[1], mg.first_unit[2], (int)grid.x, wpb, mg);
 }
 
 template <int TYPE, int NT>
@@ -862,7 +855,8 @@ static void launch1(const MatGroup& mg, const uint8_t* xq, int G, int nt, int rp
 //   Q6_K  from 3 tokens (2 tokens: 12.1 against 13.7); below 4096 rows from 5 tokens (N = 3 / 4: 1024x4096
 //         4.7 / 5.5 against 5.7 / 5.7, 2048x12288 10.8 / 12.6 against 11.4 / 11.6).
 static bool use_mfma_form(int type, int N, int G, int rows) {
-    if (G > 64) return false;
+    // (the MFMA kernels take the first workgroups of matrices 1 and 2 in 16 bits each: 16-row groups)
+    if (G > 64 || rows >= 16 * 65535) return false;
     const bool few_rows = rows < 4096;
     if (type == TYPE_Q4_K) {
         if (N == 1) return G > 16 && G <= 48 && !few_rows;

@@ -154,13 +154,17 @@ __device__ __forceinline__ T* kq_global(int64_t v) {
     return (T*)(GT*)(uintptr_t)v;
 }
 
+// bound_ctrl set (lanes whose source lies outside the row read 0): every control used here is a quad
+// permutation, a row mirror, or a row shift whose out-of-row lanes are never used, so the value is the
+// same, and the compiler can fold the move into the instruction that consumes it (one v_max_f32_dpp or
+// v_add_u32_dpp instead of a v_mov_b32_dpp and the operation).
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
-    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
 template <int CTRL>
 __device__ __forceinline__ float dppf(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
 // Sum over the 4 lanes of a quad (lanes 4j..4j+3), exact for int32.

@@ -268,8 +268,8 @@ __device__ __forceinline__ float block_value(const Q6Fields& f, const Act<TYPE_Q
 // ------------------------------------------------------------------ fp32 activations
 // The same lanes and weight fragments with fp32 activations (Kindi's q4_gemv numerics,
 // q4.cu:18-27): a lane keeps its 64 activations of the column and their sums, and per weight
-// converts the code to fp32 (v_cvt_f32_ubyte) and accumulates with fp32 FMA; per sub-block the
-// decoded scale is applied to the sum, w = (d*sc)*q - dmin*m, as
+// accumulates code * x with one fp32 multiply-add; per sub-block the decoded scale is applied to
+// the sum, w = (d*sc)*q - dmin*m, as
 //   sum_j w_j x_j = (d*sc_lo) * sum_j q_j x_j - (dmin*m_lo) * sum_j x_j   (Q4_K, likewise hi)
 //                 = (d*sc_k) * (sum_j q6u_j x_j - 32 * sum_j x_j)           (Q6_K, q6u = q + 32).
 // The quad's four partial values are added in fp32 (lanes p^1, then p^2: the same bits in the four
@@ -278,14 +278,27 @@ template <int TYPE> struct ActF;
 template <> struct ActF<TYPE_Q4_K> { float xl[32], xh[32], sxl, sxh; };   // elements 64p + 0..31, 64p + 32..63
 template <> struct ActF<TYPE_Q6_K> { float xa[64], sx[4]; };             // xa[16k + j]: element 128h + 32k + 16jj + j
 
-__device__ __forceinline__ float ubf(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xffu); }
-// acc + sum over the 4 bytes of q (codes) times x[0..3], in byte order
-__device__ __forceinline__ float dot_bytes_f32(uint32_t q, const float* x, float acc) {
-    acc = __builtin_fmaf(ubf(q, 0), x[0], acc);
-    acc = __builtin_fmaf(ubf(q, 1), x[1], acc);
-    acc = __builtin_fmaf(ubf(q, 2), x[2], acc);
-    return __builtin_fmaf(ubf(q, 3), x[3], acc);
+// Codes as f16 operands.  A 16-bit half whose value v < 1024 sits in the ten mantissa bits (exponent
+// field zero) is the f16 subnormal v * 2^-24, exactly, and v_fma_mix_f32 takes such a half as one
+// factor of an fp32 multiply-add (f16 subnormals are kept: denormal mode 3).  So a code masked into
+// a half in place, at bit 0 (value c * 2^-24) or bit 4 (c * 2^-20), needs no convert instruction, and
+// an accumulator of c * 2^-s * x terms is the fp32 accumulator of c * x scaled by 2^-s, rounding
+// step for step the same (a power-of-two scale commutes with rounding while the partial sums stay
+// at or above 2^-126 * 2^-s in magnitude; only partial sums below that, from activations near the
+// fp32 subnormal range, round differently).
+__device__ __forceinline__ float half_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)v); }
+__device__ __forceinline__ float half_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
+// acc + c0 x[0] + c1 x[1] + c2 x[2] + c3 x[3], in that order, for codes c0 = a.lo, c1 = b.lo, c2 = a.hi,
+// c3 = b.hi (each the scaled value above)
+__device__ __forceinline__ float dot_halves_f32(uint32_t a, uint32_t b, const float* x, float acc) {
+    acc = __builtin_fmaf(half_lo(a), x[0], acc);
+    acc = __builtin_fmaf(half_lo(b), x[1], acc);
+    acc = __builtin_fmaf(half_hi(a), x[2], acc);
+    return __builtin_fmaf(half_hi(b), x[3], acc);
 }
+// Bytes 0 and 2 / 1 and 3 of w in the low bytes of the two halves: [0, w.b2, 0, w.b0] / [0, w.b3, 0, w.b1].
+__device__ __forceinline__ uint32_t even_bytes(uint32_t w) { return __builtin_amdgcn_perm(w, w, 0x0c020c00u); }
+__device__ __forceinline__ uint32_t odd_bytes(uint32_t w) { return __builtin_amdgcn_perm(w, w, 0x0c030c01u); }
 
 // xg = the 256 activations of column g.
 __device__ __forceinline__ void load_act(ActF<TYPE_Q4_K>& a, const float* xg, int p) {
@@ -326,12 +339,17 @@ __device__ __forceinline__ float quad_sum_f32(float v) {
 __device__ __forceinline__ float block_value(const Frag<TYPE_Q4_K>& f, const ActF<TYPE_Q4_K>& a, int p) {
     const ScMin sm = q4k_scmin_pair(f.hdr.y, f.hdr.z, f.hdr.w, p);
     const uint32_t q[8] = {f.qa.x, f.qa.y, f.qa.z, f.qa.w, f.qb.x, f.qb.y, f.qb.z, f.qb.w};
+    // byte b of q[k] holds element 4k + b of the low half (low nibble) and of the high half (high
+    // nibble): low nibbles in place are codes * 2^-24, high nibbles in place codes * 2^-20
     float plo = 0.0f, phi = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        plo = dot_bytes_f32(q[k] & 0x0f0f0f0fu, a.xl + 4 * k, plo);
-        phi = dot_bytes_f32((q[k] >> 4) & 0x0f0f0f0fu, a.xh + 4 * k, phi);
+        const uint32_t odd = odd_bytes(q[k]);
+        plo = dot_halves_f32(q[k] & 0x000f000fu, odd & 0x000f000fu, a.xl + 4 * k, plo);
+        phi = dot_halves_f32(q[k] & 0x00f000f0u, odd & 0x00f000f0u, a.xh + 4 * k, phi);
     }
+    plo = __fmul_rn(plo, 0x1p24f);
+    phi = __fmul_rn(phi, 0x1p20f);
     const float d = f16_lo(f.hdr.x), dm = f16_hi(f.hdr.x);
     const float dsl = __fmul_rn(d, (float)sm.sc_lo), dsh = __fmul_rn(d, (float)sm.sc_hi);
     const float msl = __fmul_rn(dm, (float)sm.m_lo), msh = __fmul_rn(dm, (float)sm.m_hi);
@@ -350,11 +368,15 @@ __device__ __forceinline__ float block_value(const Q6Fields& f, const ActF<TYPE_
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         const uint32_t m4 = 0x0f0f0f0fu, m2 = 0x30303030u;
-        P[0] = dot_bytes_f32((L0[w] & m4) | ((H[w] << 4) & m2), a.xa + 0 * 16 + 4 * w, P[0]);
-        P[1] = dot_bytes_f32((L1[w] & m4) | ((H[w] << 2) & m2), a.xa + 1 * 16 + 4 * w, P[1]);
-        P[2] = dot_bytes_f32(((L0[w] >> 4) & m4) | (H[w] & m2), a.xa + 2 * 16 + 4 * w, P[2]);
-        P[3] = dot_bytes_f32(((L1[w] >> 4) & m4) | ((H[w] >> 2) & m2), a.xa + 3 * 16 + 4 * w, P[3]);
+        // four 6-bit codes per word, one per byte (elements 4w .. 4w+3 of group k), codes * 2^-24
+        const uint32_t c[4] = {(L0[w] & m4) | ((H[w] << 4) & m2), (L1[w] & m4) | ((H[w] << 2) & m2),
+                               ((L0[w] >> 4) & m4) | (H[w] & m2), ((L1[w] >> 4) & m4) | ((H[w] >> 2) & m2)};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            P[k] = dot_halves_f32(even_bytes(c[k]), odd_bytes(c[k]), a.xa + k * 16 + 4 * w, P[k]);
     }
+#pragma unroll
+    for (int k = 0; k < 4; k++) P[k] = __fmul_rn(P[k], 0x1p24f);
     const float d = f16_lo(f.dw >> (8 * f.sh));
     const int sc[4] = {sbyte(w0, jj), sbyte(w0, jj + 2), sbyte(w1, jj), sbyte(w1, jj + 2)};
     float v = 0.0f;

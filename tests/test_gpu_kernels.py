@@ -472,6 +472,20 @@ def test_gemv_f32_vs_oracle(dev, orc, ty, R, C):
     assert_close_inf(host(y), orc.matvec_f32(W, R, C, ty, x).astype(np.float64))
 
 
+@pytest.mark.parametrize("ty", [12, 14])
+@pytest.mark.parametrize("scale", [1e-20, 1e20])
+def test_gemv_f32_activation_scales(dev, orc, ty, scale):
+    """The fp32-x GEMV multiplies each code as an f16 subnormal (code * 2^-24 or 2^-20) and keeps
+    the accumulator scaled by that power of two; activations many decades from 1 stay within the
+    bar of the oracle."""
+    R, C = 1024, 4096
+    W = synth(R, C, ty, 11 + ty)
+    x = (kqq.synthetic_activations(1, C, seed=5)[0] * np.float32(scale)).astype(np.float32)
+    y = torch.empty(R, device=dev)
+    ops.gemv(dev_t(W, dev), R, C, ty, dev_t(x, dev), y)
+    assert_close_inf(host(y), orc.matvec_f32(W, R, C, ty, x).astype(np.float64))
+
+
 def test_random_shapes_sweep(dev, orc):
     """Seeded sweep over ragged shapes (R = 8..520, C = 256..8192, N = 1..16, M = 1..300, both types):
     GEMV rows within the bar of the oracle and bit-equal to their one-token results; the GEMM (both

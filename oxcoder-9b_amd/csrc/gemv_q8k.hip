@@ -30,6 +30,12 @@
 #ifndef KQ_GEMV_WAVES_PER_CU_NT2
 #define KQ_GEMV_WAVES_PER_CU_NT2 KQ_GEMV_WAVES_PER_CU   // Q4_K, two tokens per launch
 #endif
+#ifndef KQ_GEMV_WAVES_PER_CU_F32
+#define KQ_GEMV_WAVES_PER_CU_F32 KQ_GEMV_WAVES_PER_CU   // fp32 activations
+#endif
+#ifndef KQ_GEMV_WAVES_PER_CU_F32_Q6
+#define KQ_GEMV_WAVES_PER_CU_F32_Q6 KQ_GEMV_WAVES_PER_CU_Q6
+#endif
 // Q6_K on the sequential kernel: one workgroup of 4 waves per CU, one wave per SIMD, each wave
 // walking more units (4096x12288 at one token: 4 units per wave, 10.9 us against 11.6 us at 8
 // waves per CU; two tokens 12.8 against 13.9 us; 2, 3, 5 or 6 waves per CU and workgroups of 1
@@ -812,7 +818,8 @@ static void launch3(const MatGroup& mg0, const uint8_t* xq, int G, hipStream_t s
     }
     mg.first_unit[3] = total;
     const int passes = (G + 15) / 16;
-    const int wpc = TYPE == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_Q6 : NT == 2 ? KQ_GEMV_WAVES_PER_CU_NT2 : KQ_GEMV_WAVES_PER_CU;
+    const int wpc = AP::F32 ? (TYPE == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_F32_Q6 : KQ_GEMV_WAVES_PER_CU_F32)
+                    : TYPE == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_Q6 : NT == 2 ? KQ_GEMV_WAVES_PER_CU_NT2 : KQ_GEMV_WAVES_PER_CU;
     // Q6_K with one or two tokens: sequential passes (the activations are reloaded per pass,
     // which only pays off while they are few)
     // (fp32 activations keep 64 floats per lane and pass: every pass a wave of its own)

@@ -109,9 +109,11 @@ int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, fl
                 int64_t ldy, void* stream);
 
 /*
- * Up to 3 matrices sharing one Q8_K input in one launch per type (q/k/v, gate/up): the Q8_K
- * form of the CPU engine's multi-matrix gemv(m, n, A, y, x) (kcpu4.c:100-118).  C and N are
- * common; R[i], type[i], y[i] and ldy[i] per matrix.
+ * Up to 3 matrices sharing one Q8_K input in one launch per type (q/k/v, gate/up; with one token,
+ * C <= 4096 and one of the two types holding a single matrix, as a Q4_K_M layer's q, k and Q6_K v,
+ * one launch for both): the Q8_K form of the CPU engine's multi-matrix gemv(m, n, A, y, x)
+ * (kcpu4.c:100-118).  C and N are common; R[i], type[i], y[i] and ldy[i] per matrix.  Every y[i]
+ * equals kq_gemv_q8k on that matrix alone bit for bit.
  */
 int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const int* type, const void* xq,
                       int N, float* const* y, const int64_t* ldy, void* stream);

@@ -657,14 +657,15 @@ k_gemv_q8k(KQ_GEMV_HEAD, int nwaves, MatGroup mg) {
 // the workgroup merges them with the same pass tree as the sequential kernel and stores y.  With
 // one pass the value is stored directly.
 // AMAX (one matrix, one token, one pass): the argmax of the outputs as well, into *aout
-// (argmax_block.h; aws is its workspace).
-template <int TYPE, int NT, int RPW, bool AMAX, class AP = ActQ8K>
-__global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
-k_gemv_q8k_split(KQ_GEMV_HEAD, int PK, MatGroup mg, int kmax, uint8_t* aws, int* aout) {
+// (argmax_block.h; aws is its workspace).  The body takes the workgroup's index among the
+// launch's workgroups of this part (bid; the grid's own index for k_gemv_q8k_split) and the
+// pass partials' LDS (part: [stream][k][t][r][pass]).
+template <int TYPE, int NT, int RPW, bool AMAX, class AP>
+__device__ __forceinline__ void gemv_split_body(KQ_GEMV_HEAD, int PK, const MatGroup& mg, int kmax, uint8_t* aws,
+                                                int* aout, int bid, float* part) {
     using ActT = typename AP::template A<TYPE>;
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
-    extern __shared__ float part[];                    // [stream][k][t][r][pass]
     // PK = P | K << 8: P column passes, K unit streams per workgroup (the block holds K * P waves)
     const int P = PK & 0xff, K = PK >> 8;
     KQ_GEMV_PICK;
@@ -676,7 +677,7 @@ k_gemv_q8k_split(KQ_GEMV_HEAD, int PK, MatGroup mg, int kmax, uint8_t* aws, int*
     // one CU through one L2.  (Contiguous unit ranges per stream, with the streams of each XCD
     // grouped, were slower: gate+up 12.2 -> 13.1 us, the output head 95 -> 108 us.)
     const int nwg = ngrid;
-    const int lwg = blockIdx.x;
+    const int lwg = bid;
     const TileWalk<WPT> walk{lwg, nwg, stream, K};
     const int u_begin = walk.first(), u_end = total_units;
     const int p = lane & 3, slot = lane >> 2;
@@ -785,6 +786,33 @@ k_gemv_q8k_split(KQ_GEMV_HEAD, int PK, MatGroup mg, int kmax, uint8_t* aws, int*
             mg.y[mm][t * mg.ldy[mm] + rowr] = tree_final(tr);
         }
     }
+}
+
+template <int TYPE, int NT, int RPW, bool AMAX, class AP = ActQ8K>
+__global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
+k_gemv_q8k_split(KQ_GEMV_HEAD, int PK, MatGroup mg, int kmax, uint8_t* aws, int* aout) {
+    extern __shared__ float part[];
+    gemv_split_body<TYPE, NT, RPW, AMAX, AP>(w0, w1, w2, XQ, G, total_units, f1, f2, ngrid, PK, mg, kmax, aws, aout,
+                                             blockIdx.x, part);
+}
+
+// Two weight types sharing one input, one token and one column pass, in one launch: workgroups
+// [0, nwgA) run the pass-split GEMV over w0 and w1 (type TA; w1 = w0 and f1 = nA when there is
+// one), the others over w2 (type TB), each part in the unit order of its own launch, so every
+// output has the bits of the one-type launch.  The scalars keep KQ_GEMV_HEAD's slots (all
+// preloaded): total_units = nB (units of w2), f1 = first unit of w1, f2 = nA (units of type TA),
+// ngrid = both parts' workgroups; mgA / mgB hold the parts' outputs (and units for later steps).
+template <int TA, int RA, int TB, int RB>
+__global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
+k_gemv_q8k_split2(KQ_GEMV_HEAD, int nwgA, MatGroup mgA, MatGroup mgB) {
+    constexpr int PK = 1 | KQ_GEMV_WG_WAVES << 8;
+    if ((int)blockIdx.x < nwgA)
+        gemv_split_body<TA, 1, RA, false, ActQ8K>(w0, w1, w1, XQ, G, f2, f1, f2, nwgA, PK, mgA, 1, nullptr, nullptr,
+                                                  blockIdx.x, nullptr);
+    else
+        gemv_split_body<TB, 1, RB, false, ActQ8K>(w2, w2, w2, XQ, G, total_units, total_units, total_units,
+                                                  ngrid - nwgA, PK, mgB, 1, nullptr, nullptr, blockIdx.x - nwgA,
+                                                  nullptr);
 }
 
 // ------------------------------------------------------------------ launch
@@ -939,6 +967,70 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
         if (type == TYPE_Q4_K) launch1<TYPE_Q4_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q4_K, G), s);
         else launch1<TYPE_Q6_K>(mg, xg, G, nt, pick_rpw(nt, TYPE_Q6_K, G), s);
     }
+}
+
+// Both weight types sharing one input (a Q4_K_M layer's q, k and a Q6_K v): the two launches the
+// type groups would make become one (k_gemv_q8k_split2), its workgroups split between the types
+// in proportion to their weight bytes, each part's waves walking their units as the one-type
+// launch does (a 1024x4096 Q6_K matrix alone costs a launch of ~3.7 us).
+template <int TA, int RA, int TB, int RB>
+static void launch_mixed(const uint8_t* const* wa, const int* ra, float* const* ya, int na, const uint8_t* wb,
+                         int rb, float* yb, const uint8_t* xq, int G, hipStream_t s) {
+    constexpr int BSA = TA == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES, BSB = TB == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    constexpr int K = KQ_GEMV_WG_WAVES;                // one column pass: K unit streams of one wave
+    MatGroup mga{}, mgb{};
+    mga.n = na;
+    int unitsA = 0;
+    int64_t rowsA = 0;
+    for (int i = 0; i < na; i++) {
+        mga.w[i] = wa[i];
+        mga.y[i] = ya[i];
+        mga.ldy[i] = ra[i];
+        mga.first_unit[i] = unitsA;
+        unitsA += ra[i] / RA;
+        rowsA += ra[i];
+    }
+    for (int i = na; i < 4; i++) mga.first_unit[i] = unitsA;
+    const int unitsB = rb / RB;
+    mgb.n = 1;
+    mgb.w[0] = wb;
+    mgb.y[0] = yb;
+    mgb.ldy[0] = rb;
+    mgb.first_unit[0] = 0;
+    for (int i = 1; i < 4; i++) mgb.first_unit[i] = unitsB;
+    const double bytesA = (double)rowsA * BSA, bytesB = (double)rb * BSB;
+    const int streams = device_cus() * KQ_GEMV_WAVES_PER_CU;
+    int sa = (int)(streams * bytesA / (bytesA + bytesB) + 0.5);
+    sa = sa < K ? K : sa > unitsA ? unitsA : sa;
+    int sb = streams - sa;
+    sb = sb < K ? K : sb > unitsB ? unitsB : sb;
+    auto round_xcd = [](int n) { return (n + KQ_XCDS - 1) / KQ_XCDS * KQ_XCDS; };
+    const int nwga = round_xcd((sa + K - 1) / K), nwgb = round_xcd((sb + K - 1) / K);
+    hipLaunchKernelGGL((k_gemv_q8k_split2<TA, RA, TB, RB>), dim3(nwga + nwgb), dim3(64 * K), 0, s, wa[0],
+                       wa[na > 1 ? 1 : 0], wb, xq, G, unitsB, mga.first_unit[1], unitsA, nwga + nwgb, nwga, mga, mgb);
+}
+
+bool launch_gemv_q8k_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const uint8_t* xq,
+                           float* const* y, hipStream_t s) {
+    const int G = C / QK;
+    if (G > 16 || n < 2 || n > 3) return false;
+    int n4 = 0;
+    for (int i = 0; i < n; i++) n4 += type[i] == TYPE_Q4_K;
+    if (n4 == 0 || n4 == n) return false;
+    // part B: the type with one matrix (Q6_K when there is one of each)
+    const int tb = n - n4 == 1 ? TYPE_Q6_K : TYPE_Q4_K;
+    const uint8_t* wa[2];
+    int ra[2], na = 0, ib = 0;
+    float* ya[2];
+    for (int i = 0; i < n; i++) {
+        if (type[i] == tb) { ib = i; continue; }
+        wa[na] = w[i]; ra[na] = R[i]; ya[na] = y[i]; na++;
+    }
+    if (tb == TYPE_Q6_K)
+        launch_mixed<TYPE_Q4_K, 2, TYPE_Q6_K, 1>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s);
+    else
+        launch_mixed<TYPE_Q6_K, 1, TYPE_Q4_K, 2>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s);
+    return true;
 }
 
 // One token, one matrix, and the argmax of y (output head + greedy pick).  With one column pass

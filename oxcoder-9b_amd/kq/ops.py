@@ -182,8 +182,9 @@ def gemv_q8k(w, R, C_, ty, xq, N, y, ldy=None):
 
 
 def gemv_q8k_multi(mats, xq, N, ys):
-    """Up to 3 matrices [(w, R, C, type)] sharing one Q8_K input, one launch per type
-    (kq_gemv_q8k_multi).  ys[i] is [N][ld_i] or [R_i]."""
+    """Up to 3 matrices [(w, R, C, type)] sharing one Q8_K input, one launch per type, or one for
+    both types at one token and C <= 4096 when one type has a single matrix (kq_gemv_q8k_multi).
+    ys[i] is [N][ld_i] or [R_i]."""
     n = len(mats)
     if not 1 <= n <= 3 or len(ys) != n:
         raise ValueError("1..3 matrices with one output each")

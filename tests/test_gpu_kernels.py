@@ -256,6 +256,34 @@ def test_gemv_q8k_multi_matches_single(dev, orc, C, N):
         assert_close_inf(got[:, :R], orc.gemv_q8k(W, R, C_, ty, xq, N))
 
 
+@pytest.mark.parametrize("shapes,C", [
+    (((4096, 12), (1024, 12), (1024, 14)), 4096),    # a Q4_K_M layer's q, k and Q6_K v
+    (((4096, 12), (1024, 14)), 4096),                # one of each
+    (((1024, 14), (2048, 14), (4096, 12)), 4096),    # two Q6_K and one Q4_K
+    (((40, 12), (8, 14), (96, 12)), 256),            # a few tiles, one super-block
+    (((16, 14), (4104, 12)), 2048),                  # G = 8, R % 16 = 8
+    (((12288, 12), (8, 14)), 3840),                  # G = 15, a one-tile second type
+])
+def test_gemv_q8k_multi_mixed_types_one_token(dev, orc, shapes, C):
+    """One token over matrices of both types sharing an input (C <= 4096): one launch holds both
+    types' waves, and every output equals the one-matrix call bit for bit, columns past R untouched."""
+    print("multi mixed", shapes, C, flush=True)
+    mats_h = [(synth(R, C, ty, 70 + i), R, C, ty) for i, (R, ty) in enumerate(shapes)]
+    mats = [(dev_t(W, dev), R, C_, ty) for (W, R, C_, ty) in mats_h]
+    xq = orc.quantize_q8k(kqq.synthetic_activations(1, C, seed=C + 3))
+    xqd = dev_t(xq, dev)
+    ys = [torch.full((R + 4,), -7.0, device=dev) for (_, R, _, _) in mats]
+    ops.gemv_q8k_multi(mats, xqd, 1, ys)
+    for (w, R, C_, ty), y, (W, _, _, _) in zip(mats, ys, mats_h):
+        ref = torch.empty(R, device=dev)
+        ops.gemv_q8k(w, R, C_, ty, xqd, 1, ref)
+        got = host(y)
+        np.testing.assert_array_equal(got[:R], host(ref))
+        assert np.all(got[R:] == -7.0)
+        if R <= 4104:
+            assert_close_inf(got[:R], orc.gemv_q8k(W, R, C_, ty, xq, 1)[0])
+
+
 @pytest.mark.parametrize("ty,R,C,M", [
     (12, 512, 4096, 64), (14, 256, 12288, 40),       # one M tile, partial
     (12, 136, 256, 300), (14, 136, 256, 300),        # R % 128 = 8, one super-block, ragged M

@@ -61,7 +61,9 @@ int kq_gemv(const void* w, int R, int C, int type, const float* x, float* y, voi
 
 /*
  * Up to 3 matrices sharing one input, as the CPU engine's gemv(m, n, A, y, x) does
- * (kcpu4.c:100-118).  C is common; R[i], type[i] per matrix.
+ * (kcpu4.c:100-118).  C is common; R[i], type[i] per matrix.  One launch per weight type (one for
+ * both when C <= 4096 and one type has a single matrix); every y[i] equals kq_gemv on that matrix
+ * bit for bit.
  */
 int kq_gemv_multi(int n, const void* const* w, const int* R, int C, const int* type,
                   const float* x, float* const* y, void* stream);

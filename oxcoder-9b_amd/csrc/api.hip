@@ -99,6 +99,12 @@ int kq_gemv_multi(int n, const void* const* w, const int* R, int C, const int* t
     }
     if (tiles > (1 << 27)) return fail(KQ_ERR_ARG, "%s: too many rows in one call", fn);
     KQ_TRY(check_ptr(x, 4, "x", fn));
+    // both weight types (a Q4_K_M layer's q, k and Q6_K v): one launch where possible
+    {
+        const uint8_t* wa[3];
+        for (int i = 0; i < n; i++) wa[i] = static_cast<const uint8_t*>(w[i]);
+        if (launch_gemv_f32_mixed(n, wa, R, type, C, x, y, as_stream(stream))) return check_launch(fn);
+    }
     // matrices of the same type share a launch
     for (int ty : {KQ_TYPE_Q4_K, KQ_TYPE_Q6_K}) {
         const uint8_t* ws[3];

@@ -802,17 +802,16 @@ k_gemv_q8k_split(KQ_GEMV_HEAD, int PK, MatGroup mg, int kmax, uint8_t* aws, int*
 // output has the bits of the one-type launch.  The scalars keep KQ_GEMV_HEAD's slots (all
 // preloaded): total_units = nB (units of w2), f1 = first unit of w1, f2 = nA (units of type TA),
 // ngrid = both parts' workgroups; mgA / mgB hold the parts' outputs (and units for later steps).
-template <int TA, int RA, int TB, int RB>
+template <int TA, int RA, int TB, int RB, class AP = ActQ8K>
 __global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
 k_gemv_q8k_split2(KQ_GEMV_HEAD, int nwgA, MatGroup mgA, MatGroup mgB) {
     constexpr int PK = 1 | KQ_GEMV_WG_WAVES << 8;
     if ((int)blockIdx.x < nwgA)
-        gemv_split_body<TA, 1, RA, false, ActQ8K>(w0, w1, w1, XQ, G, f2, f1, f2, nwgA, PK, mgA, 1, nullptr, nullptr,
-                                                  blockIdx.x, nullptr);
+        gemv_split_body<TA, 1, RA, false, AP>(w0, w1, w1, XQ, G, f2, f1, f2, nwgA, PK, mgA, 1, nullptr, nullptr,
+                                              blockIdx.x, nullptr);
     else
-        gemv_split_body<TB, 1, RB, false, ActQ8K>(w2, w2, w2, XQ, G, total_units, total_units, total_units,
-                                                  ngrid - nwgA, PK, mgB, 1, nullptr, nullptr, blockIdx.x - nwgA,
-                                                  nullptr);
+        gemv_split_body<TB, 1, RB, false, AP>(w2, w2, w2, XQ, G, total_units, total_units, total_units,
+                                              ngrid - nwgA, PK, mgB, 1, nullptr, nullptr, blockIdx.x - nwgA, nullptr);
 }
 
 // ------------------------------------------------------------------ launch
@@ -973,7 +972,7 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
 // type groups would make become one (k_gemv_q8k_split2), its workgroups split between the types
 // in proportion to their weight bytes, each part's waves walking their units as the one-type
 // launch does (a 1024x4096 Q6_K matrix alone costs a launch of ~3.7 us).
-template <int TA, int RA, int TB, int RB>
+template <int TA, int RA, int TB, int RB, class AP>
 static void launch_mixed(const uint8_t* const* wa, const int* ra, float* const* ya, int na, const uint8_t* wb,
                          int rb, float* yb, const uint8_t* xq, int G, hipStream_t s) {
     constexpr int BSA = TA == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES, BSB = TB == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
@@ -999,19 +998,20 @@ static void launch_mixed(const uint8_t* const* wa, const int* ra, float* const* 
     mgb.first_unit[0] = 0;
     for (int i = 1; i < 4; i++) mgb.first_unit[i] = unitsB;
     const double bytesA = (double)rowsA * BSA, bytesB = (double)rb * BSB;
-    const int streams = device_cus() * KQ_GEMV_WAVES_PER_CU;
+    const int streams = device_cus() * (AP::F32 ? KQ_GEMV_WAVES_PER_CU_F32 : KQ_GEMV_WAVES_PER_CU);
     int sa = (int)(streams * bytesA / (bytesA + bytesB) + 0.5);
     sa = sa < K ? K : sa > unitsA ? unitsA : sa;
     int sb = streams - sa;
     sb = sb < K ? K : sb > unitsB ? unitsB : sb;
     auto round_xcd = [](int n) { return (n + KQ_XCDS - 1) / KQ_XCDS * KQ_XCDS; };
     const int nwga = round_xcd((sa + K - 1) / K), nwgb = round_xcd((sb + K - 1) / K);
-    hipLaunchKernelGGL((k_gemv_q8k_split2<TA, RA, TB, RB>), dim3(nwga + nwgb), dim3(64 * K), 0, s, wa[0],
+    hipLaunchKernelGGL((k_gemv_q8k_split2<TA, RA, TB, RB, AP>), dim3(nwga + nwgb), dim3(64 * K), 0, s, wa[0],
                        wa[na > 1 ? 1 : 0], wb, xq, G, unitsB, mga.first_unit[1], unitsA, nwga + nwgb, nwga, mga, mgb);
 }
 
-bool launch_gemv_q8k_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const uint8_t* xq,
-                           float* const* y, hipStream_t s) {
+template <class AP>
+static bool launch_mixed_group(int n, const uint8_t* const* w, const int* R, const int* type, int C, const uint8_t* xq,
+                               float* const* y, hipStream_t s) {
     const int G = C / QK;
     if (G > 16 || n < 2 || n > 3) return false;
     int n4 = 0;
@@ -1027,10 +1027,20 @@ bool launch_gemv_q8k_mixed(int n, const uint8_t* const* w, const int* R, const i
         wa[na] = w[i]; ra[na] = R[i]; ya[na] = y[i]; na++;
     }
     if (tb == TYPE_Q6_K)
-        launch_mixed<TYPE_Q4_K, 2, TYPE_Q6_K, 1>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s);
+        launch_mixed<TYPE_Q4_K, 2, TYPE_Q6_K, 1, AP>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s);
     else
-        launch_mixed<TYPE_Q6_K, 1, TYPE_Q4_K, 2>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s);
+        launch_mixed<TYPE_Q6_K, 1, TYPE_Q4_K, 2, AP>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s);
     return true;
+}
+
+bool launch_gemv_q8k_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const uint8_t* xq,
+                           float* const* y, hipStream_t s) {
+    return launch_mixed_group<ActQ8K>(n, w, R, type, C, xq, y, s);
+}
+
+bool launch_gemv_f32_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const float* x,
+                           float* const* y, hipStream_t s) {
+    return launch_mixed_group<ActF32>(n, w, R, type, C, reinterpret_cast<const uint8_t*>(x), y, s);
 }
 
 // One token, one matrix, and the argmax of y (output head + greedy pick).  With one column pass

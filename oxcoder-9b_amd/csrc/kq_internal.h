@@ -44,6 +44,9 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
 // a single matrix; false (nothing launched) otherwise.  Outputs bit-identical to the group above.
 bool launch_gemv_q8k_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const uint8_t* xq,
                            float* const* y, hipStream_t s);
+// The same with fp32 activations.
+bool launch_gemv_f32_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const float* x,
+                           float* const* y, hipStream_t s);
 // Small-batch GEMV on MFMA (C <= 16384, N <= 16): rows bit-identical to the GEMV above.
 void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
                             int N, float* const* y, const int64_t* ldy, hipStream_t s);

@@ -49,8 +49,9 @@ def gemv(w, R, C_, ty, x, y):
 
 
 def gemv_multi(mats, x, ys):
-    """Up to 3 matrices [(w, R, C, type)] sharing fp32 x [C], one launch per type (kq_gemv_multi;
-    the multi-matrix gemv of the CPU engine, kcpu4.c:100-118)."""
+    """Up to 3 matrices [(w, R, C, type)] sharing fp32 x [C], one launch per type, or one for both
+    types at C <= 4096 when one type has a single matrix (kq_gemv_multi; the multi-matrix gemv of
+    the CPU engine, kcpu4.c:100-118)."""
     n = len(mats)
     if not 1 <= n <= 3 or len(ys) != n:
         raise ValueError("1..3 matrices with one output each")

@@ -500,6 +500,33 @@ def test_gemv_f32_vs_oracle(dev, orc, ty, R, C):
     assert_close_inf(host(y), orc.matvec_f32(W, R, C, ty, x).astype(np.float64))
 
 
+@pytest.mark.parametrize("shapes,C", [
+    (((4096, 12), (1024, 12), (1024, 14)), 4096),    # mixed types: one launch
+    (((1024, 14), (2048, 14), (4096, 12)), 4096),
+    (((40, 12), (8, 14)), 256),
+    (((4096, 12), (1024, 12), (1024, 14)), 12288),   # three passes: one launch per type
+    (((12288, 12), (12288, 12)), 4096),              # one type
+])
+def test_gemv_f32_multi_matches_single(dev, orc, shapes, C):
+    """kq_gemv_multi (fp32 activations, up to 3 matrices sharing x, both types in one launch where it
+    can) equals kq_gemv on each matrix alone bit for bit, nothing written past R."""
+    print("f32 multi", shapes, C, flush=True)
+    mats_h = [(synth(R, C, ty, 30 + i), R, C, ty) for i, (R, ty) in enumerate(shapes)]
+    mats = [(dev_t(W, dev), R, C_, ty) for (W, R, C_, ty) in mats_h]
+    x = kqq.synthetic_activations(1, C, seed=C + 9)[0]
+    xd = dev_t(x, dev)
+    ys = [torch.full((R + 4,), -7.0, device=dev) for (_, R, _, _) in mats]
+    ops.gemv_multi(mats, xd, ys)
+    for (w, R, C_, ty), y, (W, _, _, _) in zip(mats, ys, mats_h):
+        ref = torch.empty(R, device=dev)
+        ops.gemv(w, R, C_, ty, xd, ref)
+        got = host(y)
+        np.testing.assert_array_equal(got[:R], host(ref))
+        assert np.all(got[R:] == -7.0)
+        if R <= 4096:
+            assert_close_inf(got[:R], orc.matvec_f32(W, R, C_, ty, x).astype(np.float64))
+
+
 @pytest.mark.parametrize("ty", [12, 14])
 @pytest.mark.parametrize("scale", [1e-20, 1e20])
 def test_gemv_f32_activation_scales(dev, orc, ty, scale):

@@ -56,6 +56,37 @@ def test_engine_gemv_layer(layer, orc, dev, mode):
             assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max(), n
 
 
+@pytest.mark.parametrize("mode", ["q8k", "f32"])
+def test_engine_gemv_q4k_m_attention_group(dev, orc, mode):
+    """A Q4_K_M layer's attention group (Q4_K q, k and a Q6_K v, as half the real model's layers have):
+    gemv(names, x, outs) sends both types through one launch; every output equals the one-matrix
+    call bit for bit and the oracle within the bar."""
+    w = Weights(dev)
+    host = {}
+    for i, (name, R, ty) in enumerate([("attn_q", 4096, 12), ("attn_k", 1024, 12), ("attn_v", 1024, 14)]):
+        W = kqq.synthetic_matrix(R, 4096, ty, seed=40 + i)
+        host[name] = (W, R, 4096, ty)
+        w.add(name, W, R, 4096, ty)
+    eng = Engine(w, mode=mode)
+    x = kqq.synthetic_activations(1, 4096, seed=41)[0]
+    xd = torch.from_numpy(x).to(dev)
+    names = ["attn_q", "attn_k", "attn_v"]
+    outs = [torch.empty(host[n][1], device=dev) for n in names]
+    assert eng.gemv(names, xd, outs) == 1
+    for n, y in zip(names, outs):
+        one = torch.empty(host[n][1], device=dev)
+        assert eng.gemv([n], xd, [one]) == 1
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), one.cpu().numpy())
+        W, R, C_, ty = host[n]
+        if mode == "q8k":
+            want = orc.gemv_q8k(W, R, C_, ty, orc.quantize_q8k(x[None]), 1)[0]
+        else:
+            want = orc.matvec_f32(W, R, C_, ty, x).astype(np.float64)
+        got = y.cpu().numpy()
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max(), n
+
+
 def test_engine_batch_and_gemm_agree(layer, dev):
     w, _ = layer
     eng = Engine(w, mode="q8k")

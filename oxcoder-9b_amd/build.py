@@ -28,6 +28,9 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-I" + CSRC, "-I" + os.path.join(ROOT, "include"),
 ]
+# No -fgpu-flush-denormals-to-zero or fast-math: the fp32-activation GEMV multiplies each weight code as an
+# f16 subnormal (v_fma_mix_f32 with the code in a half's mantissa bits), so f16 denormals must stay on (the
+# default denormal mode 3; tests/test_gpu_exact.py fails at once otherwise).
 # Per-source extra flags.  The MFMA kernels keep their accumulators in ordinary VGPRs (the epilogue
 # reads them with VALU instructions every super-block; accumulators in AGPRs would need a copy each).
 # The decode and verify kernels (GEMV, small-batch MFMA GEMV, quantizer, producers, argmax) take their

@@ -81,6 +81,17 @@ class Runner:
         L = (C.c_int64 * n)(*[m[1] for m in mats])
         self.check(self.lib.kq_gemv_q8k_multi(n, W, Rs, mats[0][2], Ts, C.c_void_p(xq.data_ptr()), N, Y, L, s))
 
+    def gemv_x(self, mats, x, ys, xq, s):
+        """mats: [(w, R, C, type)] sharing fp32 x (one token), quantized to Q8_K inside the launch
+        (kq_gemv_q8k_x; xq receives the bytes, needed for C > 4096)."""
+        n = len(mats)
+        W = (C.c_void_p * n)(*[m[0].data_ptr() for m in mats])
+        Rs = (C.c_int * n)(*[m[1] for m in mats])
+        Ts = (C.c_int * n)(*[m[3] for m in mats])
+        Y = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+        self.check(self.lib.kq_gemv_q8k_x(n, W, Rs, mats[0][2], Ts, C.c_void_p(x.data_ptr()), Y,
+                                          C.c_void_p(xq.data_ptr()) if mats[0][2] > 4096 else None, s))
+
     def rms_q8k(self, h, res, w, D, xq, s):
         """kq_rms_q8k on one row: h += res, xq = Q8_K(RMSNorm(h) * w)."""
         self.check(self.lib.kq_rms_q8k(C.c_void_p(h.data_ptr()), C.c_void_p(res.data_ptr()), 1,
@@ -124,6 +135,15 @@ def run_step(rn, layer, xs, xqs, ys, s):
         rn.quantize(xs[slot], C_, xqs[slot], s)
         group = [(n, R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == slot]
         rn.gemv_multi([(layer[n], R, C2, ty) for n, R, C2, ty in group], xqs[slot], [ys[n] for n, *_ in group], s)
+
+
+def run_step_x(rn, layer, xs, xqs, ys, s):
+    """The same step with each 4096-column input quantized inside its GEMV launch (kq_gemv_q8k_x:
+    q+k+v, o, gate+up; the down projection's 12288 columns keep the quantizer's own launch)."""
+    for slot, C_ in enumerate(INPUT_COLS):
+        group = [(n, R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == slot]
+        rn.gemv_x([(layer[n], R, C2, ty) for n, R, C2, ty in group], xs[slot], [ys[n] for n, *_ in group],
+                  xqs[slot], s)
 
 
 def capture(torch, fn):
@@ -348,6 +368,27 @@ def batched_extra(torch, rn, dev, steps):
             nbytes = wbytes(R, C_, ty) + N * (C_ // 256) * Q8K + N * R * 4
             out["%s_N%d" % (name, N)] = {"us": round(per * 1e6, 2), "GB/s": round(nbytes / per / 1e9, 1),
                                          "TOPS": round(2 * N * R * C_ / per / 1e12, 2)}
+    return out
+
+
+def step_x_extra(torch, rn, layers, xs, xqs, ys, steps=640):
+    """The decode-layer step with the activation quantization inside the GEMV launches (kq_gemv_q8k_x
+    for the three 4096-column inputs: 5 launches per step instead of 8), beside the headline step
+    (separate quantizer launches) on the same resident layer copies.  Same algorithmic bytes."""
+    def fn(step):
+        def go():
+            s = rn.stream()
+            for lay in layers:
+                step(rn, lay, xs, xqs, ys, s)
+        return go
+    out = {}
+    for tag, step in (("quantizer_launches", run_step), ("quantize_in_gemv", run_step_x)):
+        g = capture(torch, fn(step))
+        time_graphs(torch, [g] * 2)
+        reps = max(1, steps // len(layers))
+        per = time_graphs(torch, [g] * reps) / (reps * len(layers))
+        out[tag + "_us"] = round(per * 1e6, 2)
+        out[tag + "_GB/s"] = round(step_bytes() / per / 1e9, 1)
     return out
 
 
@@ -822,7 +863,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip batched / GEMM / decode-stream extras")
     ap.add_argument("--only", choices=("single", "batched", "verify", "producers", "f32_layer", "gemm", "head",
                                        "decode_stream",
-                                       "pack", "tp_shard", "prefill_chunk"),
+                                       "pack", "tp_shard", "prefill_chunk", "step_x"),
                     help="run only this extra (no headline step, no CPU baseline) and print its JSON; for "
                          "profiling one workload")
     ap.add_argument("--pmc-workload", choices=("gemv", "gemm", "q6k"),
@@ -849,9 +890,16 @@ def main():
         pmc_workload_q6k(torch, rn, dev)
         return
     if a.only:
-        need_layers = a.only in ("verify", "producers", "f32_layer", "prefill_chunk")
+        need_layers = a.only in ("verify", "producers", "f32_layer", "prefill_chunk", "step_x")
         lay = make_layer(torch, dev, a.copies) if need_layers else None
+        if a.only == "step_x":
+            from kq import quantize as kqq
+            xs_ = [torch.from_numpy(kqq.synthetic_activations(1, c, seed=s)[0]).to(dev)
+                   for s, c in enumerate(INPUT_COLS)]
+            xqs_ = [torch.empty((c // 256) * Q8K, dtype=torch.uint8, device=dev) for c in INPUT_COLS]
+            ys_ = {name: torch.empty(R, device=dev) for name, R, _, _, _ in LAYER}
         fn = {"single": lambda: single_gemv_extra(torch, rn, dev),
+              "step_x": lambda: step_x_extra(torch, rn, lay, xs_, xqs_, ys_),
               "batched": lambda: batched_extra(torch, rn, dev, 160),
               "verify": lambda: verify_layer_extra(torch, rn, lay, dev),
               "producers": lambda: producers_extra(torch, rn, lay, dev),

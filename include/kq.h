@@ -121,6 +121,18 @@ int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const in
                       int N, float* const* y, const int64_t* ldy, void* stream);
 
 /*
+ * Batch-1 decode GEMV from fp32 activations with Q8_K arithmetic, the quantization inside the GEMV
+ * launch: gpu4.Engine.gemv(names, x, outs) (scripts/kindi_q4/kindi/gpu4.py:95-99) takes fp32 x;
+ * here up to 3 matrices sharing x (fp32[C], 16-byte aligned) in one launch per type, each
+ * workgroup quantizing x itself (the bytes of kq_q8k_quantize), instead of a quantizer launch
+ * followed by kq_gemv_q8k_multi; every y[i] equals that pair's bit for bit.  xq (C/256*292 bytes,
+ * dword aligned, or NULL) receives the Q8_K bytes; it is required for C > 4096, where the call
+ * runs the quantizer and the GEMV as two launches.
+ */
+int kq_gemv_q8k_x(int n, const void* const* w, const int* R, int C, const int* type, const float* x,
+                  float* const* y, void* xq, void* stream);
+
+/*
  * Greedy pick over the logits: *out = index of the largest y[i] (i < n), the smallest index among
  * equal largest values; NaN is never chosen and an input with no value above -1e30 gives 0.  The
  * rule of k_argmax (scripts/kindi_q4/kindi/kindi.cu:637-661), launched after the head GEMV by

@@ -205,6 +205,42 @@ int kq_gemv_q8k(const void* w, int R, int C, int type, const void* xq, int N, fl
     return check_launch(fn);
 }
 
+int kq_gemv_q8k_x(int n, const void* const* w, const int* R, int C, const int* type, const float* x,
+                  float* const* y, void* xq, void* stream) {
+    static const char* fn = "kq_gemv_q8k_x";
+    if (n < 1 || n > 3) return fail(KQ_ERR_ARG, "%s: n=%d must be 1..3", fn, n);
+    if (!w || !R || !type || !y) return fail(KQ_ERR_ARG, "%s: NULL array argument", fn);
+    int64_t tiles = 0;
+    for (int i = 0; i < n; i++) {
+        KQ_TRY(check_matrix(w[i], R[i], C, type[i], fn));
+        KQ_TRY(check_ptr(y[i], 4, "y[i]", fn));
+        tiles += R[i] / 8;
+    }
+    if (tiles > (1 << 27)) return fail(KQ_ERR_ARG, "%s: too many rows in one call", fn);
+    KQ_TRY(check_ptr(x, 16, "x", fn));
+    if (xq) KQ_TRY(check_ptr(xq, 4, "xq", fn));
+    uint8_t* xq8 = static_cast<uint8_t*>(xq);
+    if (C > 4096) {   // more than one column pass: the quantizer's own launch, then the grouped GEMV
+        if (!xq8) return fail(KQ_ERR_ARG, "%s: C=%d > 4096 needs the xq buffer", fn, C);
+        launch_q8k_quantize(x, C, C, 1, xq8, as_stream(stream));
+        const int64_t ld[3] = {R[0], n > 1 ? R[1] : 0, n > 2 ? R[2] : 0};
+        return kq_gemv_q8k_multi(n, w, R, C, type, xq8, 1, y, ld, stream);
+    }
+    bool first = true;
+    for (int ty : {KQ_TYPE_Q4_K, KQ_TYPE_Q6_K}) {
+        const uint8_t* ws[3];
+        int rs[3];
+        float* ys[3];
+        int k = 0;
+        for (int i = 0; i < n; i++)
+            if (type[i] == ty) { ws[k] = static_cast<const uint8_t*>(w[i]); rs[k] = R[i]; ys[k] = y[i]; k++; }
+        if (!k) continue;
+        launch_gemv_q8k_x_group(k, ws, rs, C, ty, x, ys, first ? xq8 : nullptr, as_stream(stream));
+        first = false;
+    }
+    return check_launch(fn);
+}
+
 int kq_gemv_q8k_multi(int n, const void* const* w, const int* R, int C, const int* type, const void* xq,
                       int N, float* const* y, const int64_t* ldy, void* stream) {
     static const char* fn = "kq_gemv_q8k_multi";

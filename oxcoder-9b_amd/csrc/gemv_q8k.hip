@@ -20,6 +20,7 @@
 #include "kq_internal.h"
 #include "q4_lanes.h"
 #include "argmax_block.h"
+#include "q8k_block.h"
 
 #ifndef KQ_GEMV_WAVES_PER_CU
 #define KQ_GEMV_WAVES_PER_CU 8
@@ -660,9 +661,13 @@ k_gemv_q8k(KQ_GEMV_HEAD, int nwaves, MatGroup mg) {
 // (argmax_block.h; aws is its workspace).  The body takes the workgroup's index among the
 // launch's workgroups of this part (bid; the grid's own index for k_gemv_q8k_split) and the
 // pass partials' LDS (part: [stream][k][t][r][pass]).
-template <int TYPE, int NT, int RPW, bool AMAX, class AP>
+// XF (one token, one column pass): the activations arrive as fp32 (X) and every workgroup quantizes
+// them to Q8_K into LDS (xs) itself, with the stand-alone quantizer's block code, while its first
+// weight loads are in flight; workgroup 0 also writes the bytes to XQO when that is not null.
+template <int TYPE, int NT, int RPW, bool AMAX, class AP, bool XF = false>
 __device__ __forceinline__ void gemv_split_body(KQ_GEMV_HEAD, int PK, const MatGroup& mg, int kmax, uint8_t* aws,
-                                                int* aout, int bid, float* part) {
+                                                int* aout, int bid, float* part, const float* X = nullptr,
+                                                uint8_t* xs = nullptr, uint8_t* XQO = nullptr) {
     using ActT = typename AP::template A<TYPE>;
     constexpr int WPT = 8 / RPW;
     constexpr int BS = TYPE == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
@@ -707,15 +712,67 @@ __device__ __forceinline__ void gemv_split_body(KQ_GEMV_HEAD, int PK, const MatG
     };
 
     ArgBest best = arg_init();                         // AMAX: the wave's best output so far (every lane)
-    if (u_begin < u_end) {
+    static_assert(!XF || (NT == 1 && !AMAX && !AP::F32), "XF: one token of Q8_K activations, no argmax");
+    if (u_begin < u_end || XF) {
+        const bool active = u_begin < u_end;           // wave-uniform
         ActT act[NT];
         Frag<TYPE> bufA[RPW], bufB[RPW];
-        int u = u_begin, k = 0, m;
-        int64_t row0;
-        const uint8_t* base = unit_base0(u, m, row0);
+        int u = u_begin, k = 0, m = 0;
+        int64_t row0 = 0;
+        const uint8_t* base = active ? unit_base0(u, m, row0) : w0;
         // the first unit's weights before the activations: the weights come from HBM, the activations
         // (written by the launch before) from the last-level cache (decode layer 37.87 -> 37.67 us)
-        if constexpr (KQ_GEMV_SPLIT_WFIRST) {
+        if constexpr (XF) {
+            // blocks wave, wave + nw, ... of x, loaded first (the quantization waits for them, the
+            // first unit's weights come later from HBM anyway), then the first unit's weights
+            constexpr int XB = 4;                      // G <= 16 blocks over the workgroup's 4 waves
+            const int nw = P * K;
+            f32x4 xv[XB];
+#ifndef KQ_XF_XFIRST
+#define KQ_XF_XFIRST 1
+#endif
+            if constexpr (!KQ_XF_XFIRST) {
+                if (active) {
+#pragma unroll
+                    for (int r = 0; r < RPW; r++) load_frag(bufA[r], base + r * BS, p);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int i = 0; i < XB; i++) {
+                const int b = wave + nw * i < G ? wave + nw * i : G - 1;
+                xv[i] = *reinterpret_cast<const f32x4_a4*>(X + b * QK + 4 * lane);
+            }
+            if constexpr (KQ_XF_XFIRST) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (active) {
+#pragma unroll
+                    for (int r = 0; r < RPW; r++) load_frag(bufA[r], base + r * BS, p);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // the wave's blocks side by side (blocks past G go to the spare slot xs[G])
+            float e[XB][4];
+            uint8_t* ob[XB];
+#pragma unroll
+            for (int i = 0; i < XB; i++) {
+                const int b = wave + nw * i;
+                e[i][0] = xv[i].x; e[i][1] = xv[i].y; e[i][2] = xv[i].z; e[i][3] = xv[i].w;
+                ob[i] = xs + (b < G ? b : G) * Q8K_BYTES;
+            }
+            q8k_blocks_store<XB>(e, lane, ob);
+            if (XQO != nullptr && bid == 0) {
+#pragma unroll
+                for (int i = 0; i < XB; i++)
+                    if (wave + nw * i < G) q8k_block_store(e[i], lane, XQO + (wave + nw * i) * Q8K_BYTES);
+            }
+            // LDS-only barrier: the weight loads issued above stay in flight
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            if (!active) return;
+            load_act(act[0], xs + gc * Q8K_BYTES, p);
+        } else if constexpr (KQ_GEMV_SPLIT_WFIRST) {
 #pragma unroll
             for (int r = 0; r < RPW; r++) load_frag(bufA[r], base + r * BS, p);
             __builtin_amdgcn_sched_barrier(0);
@@ -794,6 +851,20 @@ k_gemv_q8k_split(KQ_GEMV_HEAD, int PK, MatGroup mg, int kmax, uint8_t* aws, int*
     extern __shared__ float part[];
     gemv_split_body<TYPE, NT, RPW, AMAX, AP>(w0, w1, w2, XQ, G, total_units, f1, f2, ngrid, PK, mg, kmax, aws, aout,
                                              blockIdx.x, part);
+}
+
+// One token from fp32 activations (C <= 4096: one column pass): x quantized to Q8_K inside the
+// launch (each workgroup into its LDS, bit for bit the stand-alone quantizer's bytes), so the
+// quantizer's own launch is saved.  XQ (KQ_GEMV_HEAD's slot) carries x; xqo, when not null,
+// receives the Q8_K bytes (from workgroup 0).
+template <int TYPE, int RPW>
+__global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
+k_gemv_q8k_x(KQ_GEMV_HEAD, MatGroup mg, uint8_t* xqo) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+    constexpr int PK = 1 | KQ_GEMV_WG_WAVES << 8;
+    gemv_split_body<TYPE, 1, RPW, false, ActQ8K, true>(w0, w1, w2, XQ, G, total_units, f1, f2, ngrid, PK, mg, 1,
+                                                       nullptr, nullptr, blockIdx.x, nullptr,
+                                                       reinterpret_cast<const float*>(XQ), xs, xqo);
 }
 
 // Two weight types sharing one input, one token and one column pass, in one launch: workgroups
@@ -1041,6 +1112,37 @@ bool launch_gemv_q8k_mixed(int n, const uint8_t* const* w, const int* R, const i
 bool launch_gemv_f32_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const float* x,
                            float* const* y, hipStream_t s) {
     return launch_mixed_group<ActF32>(n, w, R, type, C, reinterpret_cast<const uint8_t*>(x), y, s);
+}
+
+// One token of fp32 activations, n (1..3) matrices of one type, C <= 4096: x quantized inside the GEMV
+// launch (k_gemv_q8k_x); xqo (nullable) receives the Q8_K bytes.  The grid is launch3's for one pass.
+void launch_gemv_q8k_x_group(int n, const uint8_t* const* w, const int* R, int C, int type, const float* x,
+                             float* const* y, uint8_t* xqo, hipStream_t s) {
+    const int G = C / QK;
+    const int rpw = type == TYPE_Q4_K ? 2 : 1;
+    MatGroup mg{};
+    mg.n = n;
+    int total = 0;
+    for (int i = 0; i < n; i++) {
+        mg.w[i] = w[i];
+        mg.y[i] = y[i];
+        mg.ldy[i] = R[i];
+        mg.first_unit[i] = total;
+        total += R[i] / rpw;
+    }
+    for (int i = n; i < 4; i++) mg.first_unit[i] = total;
+    constexpr int K = KQ_GEMV_WG_WAVES;
+    int streams = device_cus() * (type == TYPE_Q6_K ? KQ_GEMV_WAVES_PER_CU_Q6 : KQ_GEMV_WAVES_PER_CU);
+    if (streams > total) streams = total;
+    const int nwg = (((streams + K - 1) / K) + KQ_XCDS - 1) / KQ_XCDS * KQ_XCDS;
+    const size_t lds = (size_t)(G + 1) * Q8K_BYTES;   // + a spare slot for the waves' blocks past G
+    const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
+    if (type == TYPE_Q4_K)
+        hipLaunchKernelGGL((k_gemv_q8k_x<TYPE_Q4_K, 2>), dim3(nwg), dim3(64 * K), lds, s, mg.w[0], mg.w[1], mg.w[2], xb,
+                           G, total, mg.first_unit[1], mg.first_unit[2], nwg, mg, xqo);
+    else
+        hipLaunchKernelGGL((k_gemv_q8k_x<TYPE_Q6_K, 1>), dim3(nwg), dim3(64 * K), lds, s, mg.w[0], mg.w[1], mg.w[2], xb,
+                           G, total, mg.first_unit[1], mg.first_unit[2], nwg, mg, xqo);
 }
 
 // One token, one matrix, and the argmax of y (output head + greedy pick).  With one column pass

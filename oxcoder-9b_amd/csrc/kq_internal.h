@@ -47,6 +47,11 @@ bool launch_gemv_q8k_mixed(int n, const uint8_t* const* w, const int* R, const i
 // The same with fp32 activations.
 bool launch_gemv_f32_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const float* x,
                            float* const* y, hipStream_t s);
+// One token of fp32 activations, n (1..3) matrices of one type, C <= 4096: the quantization to Q8_K
+// inside the GEMV launch (bit-identical to launch_q8k_quantize + launch_gemv_q8k_group); xqo
+// (nullable) receives the Q8_K bytes.
+void launch_gemv_q8k_x_group(int n, const uint8_t* const* w, const int* R, int C, int type, const float* x,
+                             float* const* y, uint8_t* xqo, hipStream_t s);
 // Small-batch GEMV on MFMA (C <= 16384, N <= 16): rows bit-identical to the GEMV above.
 void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
                             int N, float* const* y, const int64_t* ldy, hipStream_t s);

@@ -64,4 +64,77 @@ __device__ __forceinline__ uint32_t q8k_block_store(const float (&e)[4], int lan
     return packed;
 }
 
+// NB blocks quantized by one wave at once (e[b]: this lane's values 4*lane .. 4*lane+3 of block b,
+// ob[b]: its 292 output bytes): the bytes of q8k_block_store on each block, with the blocks'
+// dependent steps (cross-lane maximum, first-maximum pick, divisions, sums) issued side by side in
+// one straight-line sequence; an all-zero block takes iscale = 0 by a select (every quant 0, d 0),
+// not a branch.
+template <int NB>
+__device__ __forceinline__ void q8k_blocks_store(const float (&e)[NB][4], int lane, uint8_t* const (&ob)[NB]) {
+    float amax[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+        amax[b] = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(e[b][0]), __builtin_fabsf(e[b][1])),
+                                  __builtin_fmaxf(__builtin_fabsf(e[b][2]), __builtin_fabsf(e[b][3])));
+#pragma unroll
+    for (int b = 0; b < NB; b++) amax[b] = __builtin_fmaxf(amax[b], dppf<DPP_QUAD_XOR1>(amax[b]));
+#pragma unroll
+    for (int b = 0; b < NB; b++) amax[b] = __builtin_fmaxf(amax[b], dppf<DPP_QUAD_XOR2>(amax[b]));
+#pragma unroll
+    for (int b = 0; b < NB; b++) amax[b] = __builtin_fmaxf(amax[b], dppf<DPP_ROW_HALF_MIRROR>(amax[b]));
+#pragma unroll
+    for (int b = 0; b < NB; b++) amax[b] = __builtin_fmaxf(amax[b], dppf<DPP_ROW_MIRROR>(amax[b]));
+#pragma unroll
+    for (int b = 0; b < NB; b++) amax[b] = xor16_max(amax[b]);
+#pragma unroll
+    for (int b = 0; b < NB; b++) amax[b] = xor32_max(amax[b]);
+    float iscale[NB], d[NB];
+    bool nz[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        float first = 0.0f;
+        bool has = false;
+#pragma unroll
+        for (int k = 3; k >= 0; k--)
+            if (__builtin_fabsf(e[b][k]) == amax[b]) { first = e[b][k]; has = true; }
+        const uint64_t holders = __ballot(has);
+        const int src = holders ? __builtin_ctzll(holders) : 0;
+        const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, first), src));
+        nz[b] = amax[b] != 0.0f;
+        iscale[b] = nz[b] ? -127.0f / vmax : 0.0f;
+        d[b] = nz[b] ? 1.0f / iscale[b] : 0.0f;
+    }
+    uint32_t packed[NB];
+    int s4[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        packed[b] = 0;
+        s4[b] = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            int q = (int)__builtin_rintf(__fmul_rn(iscale[b], e[b][k]));
+            q = !nz[b] ? 0 : q < 127 ? q : 127;
+            s4[b] += q;
+            packed[b] |= (uint32_t)(q & 0xff) << (8 * k);
+        }
+    }
+    uint32_t pair[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        s4[b] = quad_sum_i32(s4[b]);
+        const int s_next = dpp<DPP_ROW_HALF_MIRROR>(s4[b]);
+        pair[b] = ((uint32_t)s4[b] & 0xffffu) | ((uint32_t)s_next << 16);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) *reinterpret_cast<uint32_t*>(ob[b] + 4 + 4 * lane) = packed[b];
+    if (lane == 0) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) *reinterpret_cast<float*>(ob[b]) = d[b];
+    }
+    if ((lane & 7) == 0) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) *reinterpret_cast<uint32_t*>(ob[b] + 260 + 4 * (lane >> 3)) = pair[b];
+    }
+}
+
 }  // namespace kq

@@ -25,6 +25,7 @@ KQ_SYMBOLS = {
     "kq_argmax": (_i, [_vp, _i, _vp, _vp, _vp]),
     "kq_gemv_q8k_argmax": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "kq_gemv_q8k": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),
+    "kq_gemv_q8k_x": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, C.POINTER(_vp), _vp, _vp]),
     "kq_gemv_q8k_multi": (_i, [_i, C.POINTER(_vp), C.POINTER(_i), _i, C.POINTER(_i), _vp, _i,
                                C.POINTER(_vp), C.POINTER(_i64), _vp]),
     "kq_gemm_q8k": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _i64, _vp]),

@@ -11,8 +11,10 @@ for each name, ``outs[i][:R] = W_name @ x`` on the current stream, asynchronousl
 (the number of column parts, as the reference does).  Two numerics modes:
 
 * ``"f32"`` -- fp32 activations, the reference's numerics (kq_gemv).
-* ``"q8k"`` -- the input is quantized once to Q8_K (kq_q8k_quantize) into a preallocated
-  workspace, then every named matrix runs the int8 GEMV (kq_gemv_q8k).
+* ``"q8k"`` -- the input is quantized to Q8_K and every named matrix runs the int8 GEMV: for up to
+  4096 columns inside the GEMV launch itself (kq_gemv_q8k_x, one launch per three matrices), beyond
+  that once (kq_q8k_quantize) into a preallocated workspace, then kq_gemv_q8k_multi; the same bits
+  either way.
 
 ``gemv_batch`` (speculative verify, N <= 16 rows) and ``gemm`` (prefill chunk, any M) extend the
 same contract to several activation rows: X is [N][C] fp32, each out is [N][R] (row stride
@@ -168,6 +170,12 @@ class Engine:
             # matrices sharing the input go three at a time into one launch per type (kcpu4.c:100-118)
             for i in range(0, len(mats), 3):
                 ops.gemv_multi(mats[i:i + 3], x, outs[i:i + 3])
+            return 1
+        if C <= 4096 and x.is_contiguous() and x.data_ptr() % 16 == 0:
+            # one column pass: each launch quantizes x itself (kq_gemv_q8k_x, the quantizer's bytes),
+            # matrices sharing the input three at a time (kcpu4.c:100-118)
+            for i in range(0, len(mats), 3):
+                ops.gemv_q8k_x(mats[i:i + 3], x.reshape(-1), outs[i:i + 3])
             return 1
         xq = self._quantize(x.reshape(1, -1)[:, :C], C)
         # matrices sharing the input go three at a time into one launch (kcpu4.c:100-118)

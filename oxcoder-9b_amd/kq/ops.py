@@ -182,6 +182,35 @@ def gemv_q8k(w, R, C_, ty, xq, N, y, ldy=None):
     return y
 
 
+def gemv_q8k_x(mats, x, ys, xq=None):
+    """Up to 3 matrices [(w, R, C, type)] sharing one fp32 activation x[C] (16-byte aligned), one token,
+    x quantized to Q8_K inside the GEMV launch (kq_gemv_q8k_x).  ``xq`` (uint8, C/256*292 bytes)
+    receives the Q8_K bytes when given; it is required for C > 4096."""
+    n = len(mats)
+    if not 1 <= n <= 3 or len(ys) != n:
+        raise ValueError("1..3 matrices with one output each")
+    C_ = mats[0][2]
+    if any(m[2] != C_ for m in mats):
+        raise ValueError("matrices sharing an input must have the same column count")
+    if x.numel() < C_:
+        raise ValueError("x too small")
+    W = (C.c_void_p * n)(*[_weights(w, R, C_, ty).value for (w, R, _, ty) in mats])
+    Rs = (C.c_int * n)(*[m[1] for m in mats])
+    Ts = (C.c_int * n)(*[m[3] for m in mats])
+    for (w, R, _, ty), y in zip(mats, ys):
+        if y.numel() < R:
+            raise ValueError("output too small")
+    Y = (C.c_void_p * n)(*[_dev(y, "y", torch.float32).value for y in ys])
+    pq = None
+    if xq is not None:
+        if xq.numel() < (C_ // QK) * Q8K_BYTES:
+            raise ValueError("xq too small")
+        pq = _dev(xq, "xq", torch.uint8)
+    _lib.check(_lib.kq().kq_gemv_q8k_x(n, W, Rs, C_, Ts, _dev(x, "x", torch.float32), Y, pq,
+                                       _stream(mats[0][0].device)))
+    return ys
+
+
 def gemv_q8k_multi(mats, xq, N, ys):
     """Up to 3 matrices [(w, R, C, type)] sharing one Q8_K input, one launch per type, or one for
     both types at one token and C <= 4096 when one type has a single matrix (kq_gemv_q8k_multi).

@@ -284,6 +284,49 @@ def test_gemv_q8k_multi_mixed_types_one_token(dev, orc, shapes, C):
             assert_close_inf(got[:R], orc.gemv_q8k(W, R, C_, ty, xq, 1)[0])
 
 
+@pytest.mark.parametrize("shapes,C", [
+    (((4096, 12), (1024, 12), (1024, 12)), 4096),    # q, k, v
+    (((12288, 12), (12288, 12)), 4096),              # gate, up
+    (((4096, 12), (1024, 12), (1024, 14)), 4096),    # both types: one launch per type
+    (((40, 14), (8, 14)), 256),                      # one super-block
+    (((136, 12),), 3840),                            # G = 15
+    (((4096, 14),), 1024),
+    (((4096, 12), (4096, 14)), 12288),               # C > 4096: quantizer launch, then the GEMV
+])
+def test_gemv_q8k_x_matches_quantize_then_gemv(dev, orc, shapes, C):
+    """kq_gemv_q8k_x (fp32 x quantized to Q8_K inside the GEMV launch, every workgroup into its LDS)
+    equals kq_q8k_quantize followed by kq_gemv_q8k_multi bit for bit, the optional xq output equals
+    the quantizer's bytes, and nothing is written past R; with a zero block, a tied maximum and a
+    block of one repeated value in x."""
+    print("gemv_q8k_x", shapes, C, flush=True)
+    mats_h = [(synth(R, C, ty, 60 + i), R, C, ty) for i, (R, ty) in enumerate(shapes)]
+    mats = [(dev_t(W, dev), R, C_, ty) for (W, R, C_, ty) in mats_h]
+    x = kqq.synthetic_activations(1, C, seed=C + 5)[0].copy()
+    x[:256] = 0.0
+    if C >= 768:
+        x[256 + 5], x[256 + 9] = -7.0, 7.0
+        x[512:768] = 0.3
+    xd = dev_t(x, dev)
+    xq_ref = ops.q8k_quantize(xd)
+    ys = [torch.full((R + 4,), -7.0, device=dev) for (_, R, _, _) in mats]
+    xq_out = torch.full(((C // 256) * 292,), 0x55, dtype=torch.uint8, device=dev)
+    ops.gemv_q8k_x(mats, xd, ys, xq_out)
+    np.testing.assert_array_equal(host(xq_out), host(xq_ref).reshape(-1))
+    refs = [torch.empty(R, device=dev) for (_, R, _, _) in mats]
+    ops.gemv_q8k_multi(mats, xq_ref, 1, refs)
+    for (w, R, C_, ty), y, ref in zip(mats, ys, refs):
+        got = host(y)
+        np.testing.assert_array_equal(got[:R], host(ref))
+        assert np.all(got[R:] == -7.0)
+    if C <= 4096:   # without the xq output too
+        ys2 = [torch.empty(R, device=dev) for (_, R, _, _) in mats]
+        ops.gemv_q8k_x(mats, xd, ys2)
+        for y2, ref in zip(ys2, refs):
+            np.testing.assert_array_equal(host(y2), host(ref))
+    W, R, C_, ty = mats_h[0]
+    assert_close_inf(host(ys[0])[:R], orc.gemv_q8k(W, R, C_, ty, orc.quantize_q8k(x[None]), 1)[0])
+
+
 @pytest.mark.parametrize("ty,R,C,M", [
     (12, 512, 4096, 64), (14, 256, 12288, 40),       # one M tile, partial
     (12, 136, 256, 300), (14, 136, 256, 300),        # R % 128 = 8, one super-block, ragged M

@@ -12,7 +12,8 @@ HIP graphs (one graph of 32 steps plus a remainder graph) so host launch overhea
 value = algorithmic bytes per step (weights + activations read + outputs written, each once)
         / measured time per step, in GB/s.
 Also reported: the dominant kernel's roofline fraction (Q4_K GEMV, per-launch HIP events), the
-reference CPU path (kc_matvec, fp32 activations) on the host cores, speculative-verify batched
+reference CPU path (kc_matvec, fp32 activations) on the host cores, the same step with the three
+4096-column inputs quantized inside their GEMV launches (kq_gemv_q8k_x), speculative-verify batched
 GEMV (per matrix and through the layer), the fp32-activation drop-in over the same layer, the prefill GEMM, the output heads and the
 full decode weight stream.
 """
@@ -972,6 +973,8 @@ def main():
                      "avg_bytes_per_launch": round(kb), "avg_us_per_launch": round(ks * 1e6, 3)},
     }
     if not a.no_extras:
+        log("bench: the step with the quantization inside the GEMV launches")
+        result["step_quantize_in_gemv"] = step_x_extra(torch, rn, layers, xs, xqs, ys)
         log("bench: single 4096x4096 Q4_K GEMV")
         result["single_gemv_4096"] = single_gemv_extra(torch, rn, dev)
         log("bench: batched GEMV")

@@ -455,8 +455,10 @@ def producers_extra(torch, rn, layers, dev, steps=320):
     """Decode layer with the fused producers and a real layer's data dependencies: RMSNorm of the
     residual stream (adding the previous block's output) straight to Q8_K -> q/k/v; quantize the
     attention output (attention itself is not part of this path: a fixed synthetic vector) -> o;
-    RMSNorm (adding o's output) to Q8_K -> gate/up; SwiGLU of their outputs to Q8_K -> down.
-    Also the latency of one fused producer call (64 back-to-back calls in a graph)."""
+    RMSNorm (adding o's output) to Q8_K -> gate/up; SwiGLU of their outputs to Q8_K -> down.  Also
+    the same layer with the attention output quantized inside the o launch (kq_gemv_q8k_x: 7
+    launches instead of 8), and the latency of one fused producer call (64 back-to-back calls in a
+    graph)."""
     from kq import quantize as kqq
     D, F = 4096, 12288
     g = torch.Generator().manual_seed(5)
@@ -468,29 +470,34 @@ def producers_extra(torch, rn, layers, dev, steps=320):
     xd = torch.empty((F // 256) * Q8K, dtype=torch.uint8, device=dev)
     ys = {name: torch.zeros(R, device=dev) for name, R, _, _, _ in LAYER}
 
-    def step(lay, s):
+    def step(lay, s, o_in_gemv=False):
         rn.rms_q8k(h, ys["ffn_down"], w_attn, D, xa, s)
         rn.gemv_multi([(lay[n], R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == 0], xa,
                       [ys[n] for n, R, C2, ty, sl in LAYER if sl == 0], s)
-        rn.quantize(att, D, xo, s)
-        rn.gemv(lay["attn_output"], 4096, D, 12, xo, 1, ys["attn_output"], s)
+        if o_in_gemv:   # the attention output quantized inside the o launch (kq_gemv_q8k_x)
+            rn.gemv_x([(lay["attn_output"], 4096, D, 12)], att, [ys["attn_output"]], xo, s)
+        else:
+            rn.quantize(att, D, xo, s)
+            rn.gemv(lay["attn_output"], 4096, D, 12, xo, 1, ys["attn_output"], s)
         rn.rms_q8k(h, ys["attn_output"], w_ffn, D, xf, s)
         rn.gemv_multi([(lay[n], R, C2, ty) for n, R, C2, ty, sl in LAYER if sl == 2], xf,
                       [ys["ffn_gate"], ys["ffn_up"]], s)
         rn.swiglu_q8k(ys["ffn_gate"], ys["ffn_up"], F, xd, s)
         rn.gemv(lay["ffn_down"], 4096, F, 14, xd, 1, ys["ffn_down"], s)
 
-    def run_all():
-        s = rn.stream()
-        for lay in layers:
-            step(lay, s)
-
-    gr = capture(torch, run_all)
-    time_graphs(torch, [gr] * 2)
-    reps = max(1, steps // len(layers))
-    per = time_graphs(torch, [gr] * reps) / (reps * len(layers))
     wbytes_layer = sum(wbytes(R, C_, ty) for _, R, C_, ty, _ in LAYER)
-    out = {"layer_us": round(per * 1e6, 2), "weight_GB/s": round(wbytes_layer / per / 1e9, 1)}
+    out = {}
+    for tag, o_in_gemv in (("", False), ("o_quantize_in_gemv_", True)):
+        def run_all():
+            s = rn.stream()
+            for lay in layers:
+                step(lay, s, o_in_gemv)
+
+        gr = capture(torch, run_all)
+        time_graphs(torch, [gr] * 2)
+        reps = max(1, steps // len(layers))
+        per = time_graphs(torch, [gr] * reps) / (reps * len(layers))
+        out.update({tag + "layer_us": round(per * 1e6, 2), tag + "weight_GB/s": round(wbytes_layer / per / 1e9, 1)})
 
     def single(fn):
         gs = capture(torch, lambda: [fn(rn.stream()) for _ in range(64)])

@@ -732,7 +732,8 @@ def gemm_extra(torch, rn, dev, timed=True):
 
 def decode_stream_extra(torch, rn, dev):
     """Full 9B-shaped decode weight stream at batch 1: 32 layers (Q6_K attn_v and ffn_down on
-    even layers, Q4_K otherwise) + 151936x4096 Q6_K lm_head; one graph per token."""
+    even layers, Q4_K otherwise) + 151936x4096 Q6_K lm_head; one graph per token.  Also with each
+    layer's 4096-column inputs quantized inside their GEMV launches (kq_gemv_q8k_x)."""
     from kq import ops, quantize as kqq
     shapes = {}
     for i, (name, R, C_, ty, slot) in enumerate(LAYER):
@@ -753,25 +754,33 @@ def decode_stream_extra(torch, rn, dev):
     ys = {name: torch.empty(R, device=dev) for name, R, _, _, _ in LAYER}
     logits = torch.empty(151936, device=dev)
 
-    def token():
-        s = rn.stream()
-        for lay in layers:
-            for slot, c in enumerate(INPUT_COLS):
-                rn.quantize(xs[slot], c, xqs[slot], s)
-                group = [(name, v) for name, v in lay.items() if v[4] == slot]
-                rn.gemv_multi([(w, R, C_, t) for _, (w, R, C_, t, _) in group], xqs[slot],
-                              [ys[name] for name, _ in group], s)
-        rn.quantize(xs[0], 4096, xqs[0], s)
-        rn.gemv(head, 151936, 4096, 14, xqs[0], 1, logits, s)
+    def token(in_gemv):
+        def go():
+            s = rn.stream()
+            for lay in layers:
+                for slot, c in enumerate(INPUT_COLS):
+                    group = [(name, v) for name, v in lay.items() if v[4] == slot]
+                    mats = [(w, R, C_, t) for _, (w, R, C_, t, _) in group]
+                    if in_gemv:
+                        rn.gemv_x(mats, xs[slot], [ys[name] for name, _ in group], xqs[slot], s)
+                    else:
+                        rn.quantize(xs[slot], c, xqs[slot], s)
+                        rn.gemv_multi(mats, xqs[slot], [ys[name] for name, _ in group], s)
+            rn.quantize(xs[0], 4096, xqs[0], s)
+            rn.gemv(head, 151936, 4096, 14, xqs[0], 1, logits, s)
+        return go
 
-    g = capture(torch, token)
-    time_graphs(torch, [g])
-    reps = 10
-    el = time_graphs(torch, [g] * reps) / reps
+    out = {"weight_bytes_per_token": total}
+    for tag, in_gemv in (("", False), ("quantize_in_gemv_", True)):
+        g = capture(torch, token(in_gemv))
+        time_graphs(torch, [g])
+        reps = 10
+        el = time_graphs(torch, [g] * reps) / reps
+        out.update({tag + "ms_per_token": round(el * 1e3, 4), tag + "tokens_per_s": round(1 / el, 1),
+                    tag + "GB/s": round(total / el / 1e9, 1), tag + "hbm_frac": round(total / el / 1e9 / HBM_PEAK_GBS, 4)})
+        del g
     del layers, shapes, head
-    return {"weight_bytes_per_token": total, "ms_per_token": round(el * 1e3, 4),
-            "tokens_per_s": round(1 / el, 1), "GB/s": round(total / el / 1e9, 1),
-            "hbm_frac": round(total / el / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def prefill_chunk_extra(torch, rn, dev, layers, M=256):

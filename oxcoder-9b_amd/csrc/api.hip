@@ -226,6 +226,11 @@ int kq_gemv_q8k_x(int n, const void* const* w, const int* R, int C, const int* t
         const int64_t ld[3] = {R[0], n > 1 ? R[1] : 0, n > 2 ? R[2] : 0};
         return kq_gemv_q8k_multi(n, w, R, C, type, xq8, 1, y, ld, stream);
     }
+    {   // both weight types: one launch where possible
+        const uint8_t* wa[3];
+        for (int i = 0; i < n; i++) wa[i] = static_cast<const uint8_t*>(w[i]);
+        if (launch_gemv_q8k_x_mixed(n, wa, R, type, C, x, y, xq8, as_stream(stream))) return check_launch(fn);
+    }
     bool first = true;
     for (int ty : {KQ_TYPE_Q4_K, KQ_TYPE_Q6_K}) {
         const uint8_t* ws[3];

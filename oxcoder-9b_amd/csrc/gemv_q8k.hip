@@ -873,16 +873,20 @@ k_gemv_q8k_x(KQ_GEMV_HEAD, MatGroup mg, uint8_t* xqo) {
 // output has the bits of the one-type launch.  The scalars keep KQ_GEMV_HEAD's slots (all
 // preloaded): total_units = nB (units of w2), f1 = first unit of w1, f2 = nA (units of type TA),
 // ngrid = both parts' workgroups; mgA / mgB hold the parts' outputs (and units for later steps).
-template <int TA, int RA, int TB, int RB, class AP = ActQ8K>
+// XF: XQ carries fp32 x, quantized in every workgroup as in k_gemv_q8k_x (xqo: the bytes, or null).
+template <int TA, int RA, int TB, int RB, class AP = ActQ8K, bool XF = false>
 __global__ void __launch_bounds__(64 * KQ_GEMV_WG_WAVES)
-k_gemv_q8k_split2(KQ_GEMV_HEAD, int nwgA, MatGroup mgA, MatGroup mgB) {
+k_gemv_q8k_split2(KQ_GEMV_HEAD, int nwgA, MatGroup mgA, MatGroup mgB, uint8_t* xqo) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
     constexpr int PK = 1 | KQ_GEMV_WG_WAVES << 8;
+    const float* X = XF ? reinterpret_cast<const float*>(XQ) : nullptr;
     if ((int)blockIdx.x < nwgA)
-        gemv_split_body<TA, 1, RA, false, AP>(w0, w1, w1, XQ, G, f2, f1, f2, nwgA, PK, mgA, 1, nullptr, nullptr,
-                                              blockIdx.x, nullptr);
+        gemv_split_body<TA, 1, RA, false, AP, XF>(w0, w1, w1, XQ, G, f2, f1, f2, nwgA, PK, mgA, 1, nullptr, nullptr,
+                                                  blockIdx.x, nullptr, X, xs, xqo);
     else
-        gemv_split_body<TB, 1, RB, false, AP>(w2, w2, w2, XQ, G, total_units, total_units, total_units,
-                                              ngrid - nwgA, PK, mgB, 1, nullptr, nullptr, blockIdx.x - nwgA, nullptr);
+        gemv_split_body<TB, 1, RB, false, AP, XF>(w2, w2, w2, XQ, G, total_units, total_units, total_units,
+                                                  ngrid - nwgA, PK, mgB, 1, nullptr, nullptr, blockIdx.x - nwgA,
+                                                  nullptr, X, xs, nullptr);
 }
 
 // ------------------------------------------------------------------ launch
@@ -1043,9 +1047,9 @@ void launch_gemv_q8k_group(int n, const uint8_t* const* w, const int* R, int C, 
 // type groups would make become one (k_gemv_q8k_split2), its workgroups split between the types
 // in proportion to their weight bytes, each part's waves walking their units as the one-type
 // launch does (a 1024x4096 Q6_K matrix alone costs a launch of ~3.7 us).
-template <int TA, int RA, int TB, int RB, class AP>
+template <int TA, int RA, int TB, int RB, class AP, bool XF = false>
 static void launch_mixed(const uint8_t* const* wa, const int* ra, float* const* ya, int na, const uint8_t* wb,
-                         int rb, float* yb, const uint8_t* xq, int G, hipStream_t s) {
+                         int rb, float* yb, const uint8_t* xq, int G, hipStream_t s, uint8_t* xqo = nullptr) {
     constexpr int BSA = TA == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES, BSB = TB == TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     constexpr int K = KQ_GEMV_WG_WAVES;                // one column pass: K unit streams of one wave
     MatGroup mga{}, mgb{};
@@ -1076,13 +1080,15 @@ static void launch_mixed(const uint8_t* const* wa, const int* ra, float* const* 
     sb = sb < K ? K : sb > unitsB ? unitsB : sb;
     auto round_xcd = [](int n) { return (n + KQ_XCDS - 1) / KQ_XCDS * KQ_XCDS; };
     const int nwga = round_xcd((sa + K - 1) / K), nwgb = round_xcd((sb + K - 1) / K);
-    hipLaunchKernelGGL((k_gemv_q8k_split2<TA, RA, TB, RB, AP>), dim3(nwga + nwgb), dim3(64 * K), 0, s, wa[0],
-                       wa[na > 1 ? 1 : 0], wb, xq, G, unitsB, mga.first_unit[1], unitsA, nwga + nwgb, nwga, mga, mgb);
+    const size_t lds = XF ? (size_t)(G + 1) * Q8K_BYTES : 0;   // XF: the Q8_K blocks + a spare slot
+    hipLaunchKernelGGL((k_gemv_q8k_split2<TA, RA, TB, RB, AP, XF>), dim3(nwga + nwgb), dim3(64 * K), lds, s, wa[0],
+                       wa[na > 1 ? 1 : 0], wb, xq, G, unitsB, mga.first_unit[1], unitsA, nwga + nwgb, nwga, mga, mgb,
+                       xqo);
 }
 
-template <class AP>
+template <class AP, bool XF = false>
 static bool launch_mixed_group(int n, const uint8_t* const* w, const int* R, const int* type, int C, const uint8_t* xq,
-                               float* const* y, hipStream_t s) {
+                               float* const* y, hipStream_t s, uint8_t* xqo = nullptr) {
     const int G = C / QK;
     if (G > 16 || n < 2 || n > 3) return false;
     int n4 = 0;
@@ -1098,10 +1104,15 @@ static bool launch_mixed_group(int n, const uint8_t* const* w, const int* R, con
         wa[na] = w[i]; ra[na] = R[i]; ya[na] = y[i]; na++;
     }
     if (tb == TYPE_Q6_K)
-        launch_mixed<TYPE_Q4_K, 2, TYPE_Q6_K, 1, AP>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s);
+        launch_mixed<TYPE_Q4_K, 2, TYPE_Q6_K, 1, AP, XF>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s, xqo);
     else
-        launch_mixed<TYPE_Q6_K, 1, TYPE_Q4_K, 2, AP>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s);
+        launch_mixed<TYPE_Q6_K, 1, TYPE_Q4_K, 2, AP, XF>(wa, ra, ya, na, w[ib], R[ib], y[ib], xq, G, s, xqo);
     return true;
+}
+
+bool launch_gemv_q8k_x_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const float* x,
+                             float* const* y, uint8_t* xqo, hipStream_t s) {
+    return launch_mixed_group<ActQ8K, true>(n, w, R, type, C, reinterpret_cast<const uint8_t*>(x), y, s, xqo);
 }
 
 bool launch_gemv_q8k_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const uint8_t* xq,

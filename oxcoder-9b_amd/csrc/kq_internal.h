@@ -52,6 +52,10 @@ bool launch_gemv_f32_mixed(int n, const uint8_t* const* w, const int* R, const i
 // (nullable) receives the Q8_K bytes.
 void launch_gemv_q8k_x_group(int n, const uint8_t* const* w, const int* R, int C, int type, const float* x,
                              float* const* y, uint8_t* xqo, hipStream_t s);
+// The same for both weight types in one launch (as launch_gemv_q8k_mixed); false (nothing launched)
+// when the group does not have that form.
+bool launch_gemv_q8k_x_mixed(int n, const uint8_t* const* w, const int* R, const int* type, int C, const float* x,
+                             float* const* y, uint8_t* xqo, hipStream_t s);
 // Small-batch GEMV on MFMA (C <= 16384, N <= 16): rows bit-identical to the GEMV above.
 void launch_gemv_mfma_group(int n, const uint8_t* const* w, const int* R, int C, int type, const uint8_t* xq,
                             int N, float* const* y, const int64_t* ldy, hipStream_t s);

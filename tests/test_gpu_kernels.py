@@ -287,7 +287,7 @@ def test_gemv_q8k_multi_mixed_types_one_token(dev, orc, shapes, C):
 @pytest.mark.parametrize("shapes,C", [
     (((4096, 12), (1024, 12), (1024, 12)), 4096),    # q, k, v
     (((12288, 12), (12288, 12)), 4096),              # gate, up
-    (((4096, 12), (1024, 12), (1024, 14)), 4096),    # both types: one launch per type
+    (((4096, 12), (1024, 12), (1024, 14)), 4096),    # both types in one launch
     (((40, 14), (8, 14)), 256),                      # one super-block
     (((136, 12),), 3840),                            # G = 15
     (((4096, 14),), 1024),

@@ -292,6 +292,7 @@ def test_gemv_q8k_multi_mixed_types_one_token(dev, orc, shapes, C):
     (((136, 12),), 3840),                            # G = 15
     (((4096, 14),), 1024),
     (((4096, 12), (4096, 14)), 12288),               # C > 4096: quantizer launch, then the GEMV
+    (((1024, 14), (2048, 14)), 8448),                # G = 33
 ])
 def test_gemv_q8k_x_matches_quantize_then_gemv(dev, orc, shapes, C):
     """kq_gemv_q8k_x (fp32 x quantized to Q8_K inside the GEMV launch, every workgroup into its LDS)

@@ -761,15 +761,15 @@ __device__ __forceinline__ void gemv_split_body(KQ_GEMV_HEAD, int PK, const MatG
                 ob[i] = xs + (b < G ? b : G) * Q8K_BYTES;
             }
             q8k_blocks_store<XB>(e, lane, ob);
-            if (XQO != nullptr && bid == 0) {
-#pragma unroll
-                for (int i = 0; i < XB; i++)
-                    if (wave + nw * i < G) q8k_block_store(e[i], lane, XQO + (wave + nw * i) * Q8K_BYTES);
-            }
             // LDS-only barrier: the weight loads issued above stay in flight
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            if (XQO != nullptr && bid == 0) {          // the bytes out of this workgroup's LDS
+                const uint32_t* src = reinterpret_cast<const uint32_t*>(xs);
+                uint32_t* dst = reinterpret_cast<uint32_t*>(XQO);
+                for (int i = threadIdx.x; i < G * (Q8K_BYTES / 4); i += 64 * nw) dst[i] = src[i];
+            }
             if (!active) return;
             load_act(act[0], xs + gc * Q8K_BYTES, p);
         } else if constexpr (KQ_GEMV_SPLIT_WFIRST) {

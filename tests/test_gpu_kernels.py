@@ -328,6 +328,29 @@ def test_gemv_q8k_x_matches_quantize_then_gemv(dev, orc, shapes, C):
     assert_close_inf(host(ys[0])[:R], orc.gemv_q8k(W, R, C_, ty, orc.quantize_q8k(x[None]), 1)[0])
 
 
+def test_gemv_q8k_x_special_values_bytes(dev):
+    """The in-launch quantization (four blocks per wave side by side, a zero block by a select) writes
+    the stand-alone quantizer's bytes for blocks holding NaN, +-inf, subnormals, signed zeros, a
+    NaN among zeros and values at the rounding edges."""
+    C = 4096
+    x = kqq.synthetic_activations(1, C, seed=17)[0].copy()
+    x[0:256] = 0.0
+    x[3] = np.nan                                     # a NaN among zeros
+    x[256:512] = np.float32(1e-40) * np.arange(256)   # subnormals
+    x[512 + 7] = np.inf
+    x[768 + 1] = -np.inf
+    x[1024:1280] = -0.0
+    x[1280 + 9] = np.nan
+    x[1536:1792] = (np.arange(256) - 128) * np.float32(0.5)  # exact halves: round-half-even after scaling
+    x[1792:2048] = 127.0 * np.sign(np.arange(256) - 100.5).astype(np.float32)
+    xd = dev_t(x, dev)
+    ref = host(ops.q8k_quantize(xd)).reshape(-1)
+    W = dev_t(synth(1024, C, 12, 3), dev)
+    out = torch.full(((C // 256) * 292,), 0x55, dtype=torch.uint8, device=dev)
+    ops.gemv_q8k_x([(W, 1024, C, 12)], xd, [torch.empty(1024, device=dev)], out)
+    np.testing.assert_array_equal(host(out), ref)
+
+
 @pytest.mark.parametrize("ty,R,C,M", [
     (12, 512, 4096, 64), (14, 256, 12288, 40),       # one M tile, partial
     (12, 136, 256, 300), (14, 136, 256, 300),        # R % 128 = 8, one super-block, ragged M

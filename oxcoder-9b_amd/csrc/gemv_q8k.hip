@@ -56,6 +56,9 @@
 #ifndef KQ_GEMV_SPLIT_MAX
 #define KQ_GEMV_SPLIT_MAX 4      // most column passes handled by the pass-split kernel (Q4_K)
 #endif
+#ifndef KQ_XF_XFIRST
+#define KQ_XF_XFIRST 1           // in-launch quantization: x's loads before the first unit's weights
+#endif
 #ifndef KQ_GEMV_SPLIT_MAX_Q6
 #define KQ_GEMV_SPLIT_MAX_Q6 2   // Q6_K, 1-2 tokens: 3-4 passes run faster as sequential passes (measured)
 #endif
@@ -728,9 +731,6 @@ __device__ __forceinline__ void gemv_split_body(KQ_GEMV_HEAD, int PK, const MatG
             constexpr int XB = 4;                      // G <= 16 blocks over the workgroup's 4 waves
             const int nw = P * K;
             f32x4 xv[XB];
-#ifndef KQ_XF_XFIRST
-#define KQ_XF_XFIRST 1
-#endif
             if constexpr (!KQ_XF_XFIRST) {
                 if (active) {
 #pragma unroll

@@ -633,6 +633,10 @@ def test_random_shapes_sweep(dev, orc):
         n = int(rng.integers(0, N))
         ops.gemv_q8k(Wd, R, C, ty, xqd[n:n + 1], 1, y1)
         assert np.array_equal(host(y1), host(yb)[n]), tag
+        if C <= 4096:   # the same row with its quantization inside the GEMV launch
+            yx = torch.empty(R, device=dev)
+            ops.gemv_q8k_x([(Wd, R, C, ty)], dev_t(np.ascontiguousarray(X[n]), dev), [yx])
+            assert np.array_equal(host(yx), host(y1)), tag
         refm = orc.gemv_q8k(W, R, C, ty, xq[:M], M)
         ym = torch.empty((M, R), device=dev)
         ops.gemm_q8k(Wd, R, C, ty, xqd, M, ym)

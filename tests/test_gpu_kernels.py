@@ -610,8 +610,9 @@ def test_gemv_f32_activation_scales(dev, orc, ty, scale):
 
 def test_random_shapes_sweep(dev, orc):
     """Seeded sweep over ragged shapes (R = 8..520, C = 256..8192, N = 1..16, M = 1..300, both types):
-    GEMV rows within the bar of the oracle and bit-equal to their one-token results; the GEMM (both
-    entry points, split or not) within the bar."""
+    GEMV rows within the bar of the oracle and bit-equal to their one-token results; the fp32-activation
+    GEMV within the bar of q4_dot's restatement; the GEMM (both entry points, split or not) within the
+    bar."""
     rng = np.random.default_rng(2024)
     for case in range(24):
         ty = (12, 14)[case % 2]
@@ -637,6 +638,9 @@ def test_random_shapes_sweep(dev, orc):
             yx = torch.empty(R, device=dev)
             ops.gemv_q8k_x([(Wd, R, C, ty)], dev_t(np.ascontiguousarray(X[n]), dev), [yx])
             assert np.array_equal(host(yx), host(y1)), tag
+        yf = torch.empty(R, device=dev)     # fp32 activations (Kindi numerics)
+        ops.gemv(Wd, R, C, ty, dev_t(np.ascontiguousarray(X[n]), dev), yf)
+        assert_close_inf(host(yf), orc.matvec_f32(W, R, C, ty, X[n]).astype(np.float64))
         refm = orc.gemv_q8k(W, R, C, ty, xq[:M], M)
         ym = torch.empty((M, R), device=dev)
         ops.gemm_q8k(Wd, R, C, ty, xqd, M, ym)

@@ -284,3 +284,15 @@ def test_argmax_workspace_size_in_the_docs():
         text = open(os.path.join(ROOT, doc)).read()
         stated = {int(v) for v in re.findall(r"kq_argmax_workspace\(\)`? bytes \((\d+)", text)}
         assert stated == {n}, (doc, stated, n)
+
+
+def test_integration_table_lists_every_entry_point():
+    """The integration guide's ABI table has a row for every function include/kq.h declares, and
+    names no function the header lacks."""
+    names = set(_declared("kq.h"))
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    listed = set()
+    for line in text.splitlines():
+        if line.startswith("| `kq_"):
+            listed |= set(re.findall(r"(kq_\w+)\(", line.split("|")[1]))
+    assert listed == names, (sorted(names - listed), sorted(listed - names))

@@ -296,3 +296,23 @@ def test_integration_table_lists_every_entry_point():
         if line.startswith("| `kq_"):
             listed |= set(re.findall(r"(kq_\w+)\(", line.split("|")[1]))
     assert listed == names, (sorted(names - listed), sorted(listed - names))
+
+
+@pytest.mark.parametrize("n,C,x,xq,msg", [
+    (0, 4096, 64, None, "n=0 must be 1..3"),
+    (1, 4096, 8, None, "x must be 16-byte aligned"),
+    (1, 4096, 64, 2, "xq must be 4-byte aligned"),
+    (1, 8192, 64, None, "C=8192 > 4096 needs the xq buffer"),
+])
+def test_gemv_q8k_x_argument_errors(n, C, x, xq, msg):
+    """kq_gemv_q8k_x checks its count, the activation and Q8_K buffer alignment, and the xq buffer that
+    more than one column pass needs, before any launch (host-only path; the pointers are never read)."""
+    from kq import _lib
+    lib = _lib.kq()
+    W = (ctypes.c_void_p * 1)(16)
+    R = (ctypes.c_int * 1)(16)
+    T = (ctypes.c_int * 1)(12)
+    Y = (ctypes.c_void_p * 1)(64)
+    rc = lib.kq_gemv_q8k_x(n, W, R, C, T, ctypes.c_void_p(x), Y, None if xq is None else ctypes.c_void_p(xq), None)
+    assert rc == _lib.KQ_ERR_ARG
+    assert msg in lib.kq_last_error().decode()

@@ -988,36 +988,33 @@ def main():
                      "launches": kn,
                      "avg_bytes_per_launch": round(kb), "avg_us_per_launch": round(ks * 1e6, 3)},
     }
+    def extra(key, msg, fn):
+        # an extra that raises is recorded as such; the headline figures above stand
+        log("bench: " + msg)
+        try:
+            result[key] = fn()
+        except Exception as e:      # noqa: BLE001
+            log("bench: %s failed: %r" % (key, e))
+            result[key] = {"error": repr(e)}
+
     if not a.no_extras:
-        log("bench: the step with the quantization inside the GEMV launches")
-        result["step_quantize_in_gemv"] = step_x_extra(torch, rn, layers, xs, xqs, ys)
-        log("bench: single 4096x4096 Q4_K GEMV")
-        result["single_gemv_4096"] = single_gemv_extra(torch, rn, dev)
-        log("bench: batched GEMV")
-        result["batched_gemv"] = batched_extra(torch, rn, dev, 160)
-        log("bench: speculative verify through a layer")
-        result["verify_layer"] = verify_layer_extra(torch, rn, layers, dev)
-        log("bench: fused producers")
-        result["producers"] = producers_extra(torch, rn, layers, dev)
-        log("bench: fp32-activation layer")
-        result["f32_layer"] = f32_layer_extra(torch, rn, layers, dev)
-        log("bench: prefill GEMM")
-        result["prefill_gemm"] = gemm_extra(torch, rn, dev)
-        log("bench: prefill chunk through a layer")
-        result["prefill_chunk_layer"] = prefill_chunk_extra(torch, rn, dev, layers)
+        extra("step_quantize_in_gemv", "the step with the quantization inside the GEMV launches",
+              lambda: step_x_extra(torch, rn, layers, xs, xqs, ys))
+        extra("single_gemv_4096", "single 4096x4096 Q4_K GEMV", lambda: single_gemv_extra(torch, rn, dev))
+        extra("batched_gemv", "batched GEMV", lambda: batched_extra(torch, rn, dev, 160))
+        extra("verify_layer", "speculative verify through a layer", lambda: verify_layer_extra(torch, rn, layers, dev))
+        extra("producers", "fused producers", lambda: producers_extra(torch, rn, layers, dev))
+        extra("f32_layer", "fp32-activation layer", lambda: f32_layer_extra(torch, rn, layers, dev))
+        extra("prefill_gemm", "prefill GEMM", lambda: gemm_extra(torch, rn, dev))
+        extra("prefill_chunk_layer", "prefill chunk through a layer", lambda: prefill_chunk_extra(torch, rn, dev, layers))
         del layers
         torch.cuda.empty_cache()
-        log("bench: output head")
-        result["head"] = head_extra(torch, rn, dev)
-        log("bench: full decode stream")
-        result["decode_stream"] = decode_stream_extra(torch, rn, dev)
-        log("bench: pack loading")
-        result["pack_load"] = pack_extra(torch, dev)
-        log("bench: one GPU's share of the layer at TP8")
-        result["tp8_shard_layer"] = tp_shard_extra(torch, rn, dev)
+        extra("head", "output head", lambda: head_extra(torch, rn, dev))
+        extra("decode_stream", "full decode stream", lambda: decode_stream_extra(torch, rn, dev))
+        extra("pack_load", "pack loading", lambda: pack_extra(torch, dev))
+        extra("tp8_shard_layer", "one GPU's share of the layer at TP8", lambda: tp_shard_extra(torch, rn, dev))
     if not a.no_cpu:
-        log("bench: CPU baseline")
-        result["cpu_baseline"] = cpu_baseline()
+        extra("cpu_baseline", "CPU baseline", cpu_baseline)
     print(json.dumps(result), flush=True)
 
 
